@@ -1,0 +1,186 @@
+/*
+ * polykernel_amd.h -- C-ABI of the MI355X (gfx950) fused transformer-block
+ * kernels.  Drop-in for the reference's launch_* host entry points.
+ *
+ * Conventions (all entry points):
+ *   - bf16 tensors travel as raw uint16_t bits (RNE), row-major, leading dims
+ *     flattened by the caller; weight matrices are [K, N] with N contiguous,
+ *     exactly the reference layouts (no hidden pre-pack).
+ *   - Every pointer is a device pointer the caller allocated; launchers never
+ *     allocate or free, except the few entry points whose reference signature
+ *     has no workspace argument (marked "library workspace" below): those keep
+ *     one lazily grown per-device buffer owned by the library.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream); every
+ *     launch is asynchronous on it.
+ *   - Return value: PK_OK (0) on success, a negative PK_ERR_* otherwise; the
+ *     message is available from pk_last_error() (thread-local).  Nothing in the
+ *     library aborts the process.
+ */
+#ifndef POLYKERNEL_AMD_H
+#define POLYKERNEL_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define PK_API __attribute__((visibility("default")))
+#else
+#define PK_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_OK 0
+#define PK_ERR_INVALID_ARG -1
+#define PK_ERR_LAUNCH -2
+#define PK_ERR_WORKSPACE -3
+#define PK_ERR_NO_DEVICE -4
+#define PK_ERR_UNSUPPORTED -5
+#define PK_ERR_HIP -6
+
+/* ---- library / device -------------------------------------------------- */
+
+/* Library version string, e.g. "polykernel_amd 0.1.0 gfx950". */
+PK_API const char *pk_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+PK_API const char *pk_last_error(void);
+/* Optional eager set-up of the current device (GELU table); every launcher
+ * also does it lazily on first use. */
+PK_API int pk_init(void);
+/* Bare gfx token of device `ordinal` ("gfx950"), written to buf.  Mirrors
+ * lib/Runtime/DeviceDetect.cpp:28-50 + 79-84 of the reference. */
+PK_API int pk_device_arch(int ordinal, char *buf, int buf_len);
+/* Parse a raw gcnArchName ("gfx950:sramecc+:xnack-") into its gfx token.
+ * Mirrors ParseGcnArchName, lib/Runtime/DeviceDetect.cpp:28-50. */
+PK_API int pk_parse_gcn_arch_name(const char *gcn_arch_name, char *buf, int buf_len);
+
+/* ---- reference entry points (same names and argument order) ------------ */
+
+/* y = bf16(x / sqrt(mean(x^2) + eps) [* w]); w may be NULL.
+ * Replaces launch_rmsnorm, kernels/generated/rmsnorm.cu:106-108. */
+PK_API int launch_rmsnorm(const uint16_t *input, const uint16_t *weight, uint16_t *output,
+                   int rows, int cols, float eps, void *stream);
+
+/* Exact erf GELU, bit-exact with kernels/cpu/cpu_reference.cpp:46-55.
+ * Replaces launch_gelu, kernels/generated/gelu.cu:56. */
+PK_API int launch_gelu(const uint16_t *input, uint16_t *output, int n, void *stream);
+
+/* C[M,N] = bf16(A[M,K] @ B[K,N]), fp32 accumulate on bf16 MFMA.
+ * Replaces launch_matmul, kernels/generated/matmul.cu:78-79. */
+PK_API int launch_matmul(const uint16_t *A, const uint16_t *B, uint16_t *C, int M, int N, int K,
+                  void *stream);
+
+/* Row softmax over the last axis.
+ * Replaces launch_softmax, kernels/generated/softmax.cu:119-120. */
+PK_API int launch_softmax(const uint16_t *input, uint16_t *output, int rows, int cols, void *stream);
+
+/* out = matmul(rmsnorm(input, eps), weight), no gamma.
+ * Replaces launch_fused_rmsnorm_matmul, kernels/generated/fused_rmsnorm_matmul.cu:114-116.
+ * The normalised 32-row panel stays in LDS when K % 64 == 0 and K <= 1536;
+ * otherwise it is staged once in library workspace. */
+PK_API int launch_fused_rmsnorm_matmul(const uint16_t *input, const uint16_t *weight, uint16_t *output,
+                                int M, int N, int K, float eps, void *stream);
+
+/* out = gelu(bias(matmul(a, b), bias)), per-stage bf16 as the reference.
+ * Replaces launch_fused_matmul_bias_gelu, kernels/generated/fused_matmul_bias_gelu.cu:104-106. */
+PK_API int launch_fused_matmul_bias_gelu(const uint16_t *a, const uint16_t *b, const uint16_t *bias,
+                                  uint16_t *output, int M, int N, int K, void *stream);
+
+/* Causal/non-causal SDPA, Q [B,H,S_q,D], K/V [B,H,S_kv,D], O [B,H,S_q,D].
+ * Query i attends to keys j <= S_kv - S_q + i when causal.
+ * Replaces launch_attention_prefill, kernels/generated/attention_prefill.cu:169-172. */
+PK_API int launch_attention_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O,
+                             int B, int H, int S_q, int S_kv, int D, float scale, int causal,
+                             void *stream);
+
+/* out [B,H,S_cache+S_new,D] = concat(cache, new_rows) along the sequence axis.
+ * Replaces launch_kv_cache_update, kernels/generated/kv_cache_update.cu:67-69. */
+PK_API int launch_kv_cache_update(const uint16_t *cache, const uint16_t *new_rows, uint16_t *out, int B,
+                           int H, int S_cache, int S_new, int D, void *stream);
+
+/* C = bf16(A @ dequant(Wq, scale)), A bf16 [M,K], Wq int8 [K,N], scale fp32 [N].
+ * Replaces launch_matmul_int8, kernels/generated/matmul_int8.cu:97-98.
+ * Library workspace (split-K partials) for long-K decode shapes. */
+PK_API int launch_matmul_int8(const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C,
+                       int M, int N, int K, void *stream);
+
+/* ---- fused ops the reference has only as golden compositions ----------- */
+
+/* out = rmsnorm(bf16(x + r), gamma, eps); gamma may be NULL.
+ * tests/golden/golden.py:108-112; IR op PolyKernelOps.td:336-346. */
+PK_API int launch_fused_residual_rmsnorm(const uint16_t *x, const uint16_t *r, const uint16_t *gamma,
+                                  uint16_t *out, int rows, int cols, float eps, void *stream);
+
+/* out = softmax(bf16(bf16(logits) + mask)), logits fp32, mask bf16 additive
+ * (0 / -inf), same shape.  tests/golden/golden.py:115-117. */
+PK_API int launch_fused_softmax_mask(const float *logits, const uint16_t *mask, uint16_t *out, int rows,
+                              int cols, void *stream);
+
+/* out = matmul(rmsnorm(x, gamma, eps), W); gamma may be NULL.
+ * tests/golden/golden.py:96-100.  Same LDS / library-workspace rule. */
+PK_API int launch_fused_rmsnorm_matmul_gamma(const uint16_t *x, const uint16_t *gamma, const uint16_t *W,
+                                      uint16_t *out, int M, int N, int K, float eps, void *stream);
+
+/* out = add(bias(matmul(a, b), bias), residual); bias may be NULL.
+ * Chain of tests/e2e/test_mlp_correctness.py:117-126 (golden.py:48-60). */
+PK_API int launch_fused_matmul_bias_residual(const uint16_t *a, const uint16_t *b, const uint16_t *bias,
+                                      const uint16_t *residual, uint16_t *out, int M, int N, int K,
+                                      void *stream);
+
+/* In-place KV append + causal prefill.  Kc/Vc hold S_cache valid rows per
+ * (b,h) with room for `cache_capacity` rows; Kn/Vn [B,H,S_q,D] are written at
+ * rows [S_cache, S_cache+S_q) and attention runs over S_kv = S_cache + S_q.
+ * golden fused_kv_append_attention, tests/golden/golden.py:139-172. */
+PK_API int launch_fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc,
+                                     const uint16_t *Kn, const uint16_t *Vn, uint16_t *O, int B,
+                                     int H, int S_q, int S_cache, int D, int cache_capacity,
+                                     float scale, int causal, void *stream);
+
+/* Symmetric per-output-channel int8 quantisation of bf16 W [K,N]; bit-exact
+ * with tests/golden/quant_golden.py:71-83. */
+PK_API int launch_quantize_int8_per_channel(const uint16_t *W, int8_t *Wq, float *scale, int K, int N,
+                                     void *stream);
+
+/* Config-2 MLP block: y = add(bias(matmul(gelu(bias(matmul(rmsnorm(x, gamma),
+ * W1), b1)), W2), b2), x).  x [M,d], W1 [d,F], W2 [F,d].  `workspace` must
+ * hold pk_mlp_block_workspace_size(M, d, F) bytes. */
+PK_API size_t pk_mlp_block_workspace_size(int M, int d, int F);
+PK_API int launch_mlp_block(const uint16_t *x, const uint16_t *gamma, const uint16_t *W1,
+                     const uint16_t *b1, const uint16_t *W2, const uint16_t *b2, uint16_t *out,
+                     int M, int d, int F, float eps, void *workspace, size_t workspace_bytes,
+                     void *stream);
+
+/* Config-5 int8 decode MLP: y = add(matmul_int8(gelu(matmul_int8(x, W1q, s1)),
+ * W2q, s2), x).  `workspace` must hold pk_decode_mlp_int8_workspace_size bytes. */
+PK_API size_t pk_decode_mlp_int8_workspace_size(int M, int d, int F);
+PK_API int launch_decode_mlp_int8(const uint16_t *x, const int8_t *W1q, const float *s1,
+                           const int8_t *W2q, const float *s2, uint16_t *out, int M, int d, int F,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
+/* Tuning/test hook: one GEMM with an explicit epilogue (0 none, 1 bias+GELU,
+ * 2 bias+residual, 3 residual) and tile (0: 256x256, 1: 128x128, 2: 64x64,
+ * -1: heuristic).  Same numerics as the entry points above. */
+PK_API int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C,
+                      const uint16_t *bias, const uint16_t *R, int M, int N, int K, int tile,
+                      void *stream);
+
+/* ---- synthetic inputs (host, deterministic, OpenMP) -------------------- */
+
+/* out[i] = bf16 RNE of float(mean + std * z_i), z_i standard normal from the
+ * counter-based generator (SplitMix64 -> Box-Muller in double) at (seed,
+ * stream_id, i).  Identical output for any thread count. */
+PK_API void pk_synth_normal_bf16(uint64_t seed, uint64_t stream_id, double mean, double std, uint16_t *out,
+                          int64_t n);
+/* Same draws, kept as fp32. */
+PK_API void pk_synth_normal_f32(uint64_t seed, uint64_t stream_id, double mean, double std, float *out,
+                         int64_t n);
+/* Additive bf16 mask: -inf (0xFF80) with probability p, else +0. */
+PK_API void pk_synth_mask_bf16(uint64_t seed, uint64_t stream_id, double p, uint16_t *out, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POLYKERNEL_AMD_H */

@@ -1,0 +1,102 @@
+"""ctypes binding of libpolykernel_amd.so (the C-ABI of include/polykernel_amd.h).
+
+The library is loaded from the package directory only.  If it is missing the
+import fails loudly -- there is no CPU fallback for any kernel.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libpolykernel_amd.so"
+
+PK_OK = 0
+PK_ERR_INVALID_ARG = -1
+PK_ERR_LAUNCH = -2
+PK_ERR_WORKSPACE = -3
+PK_ERR_NO_DEVICE = -4
+PK_ERR_UNSUPPORTED = -5
+PK_ERR_HIP = -6
+
+
+class PolyKernelError(RuntimeError):
+    """A launcher returned a non-zero status; carries the library's message."""
+
+    def __init__(self, name: str, code: int, message: str):
+        super().__init__(f"{name} failed with status {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+P = C.c_void_p
+I = C.c_int
+F = C.c_float
+SZ = C.c_size_t
+U64 = C.c_uint64
+I64 = C.c_int64
+D = C.c_double
+
+# name -> (restype, argtypes); mirrors include/polykernel_amd.h
+SIGNATURES = {
+    "pk_version": (C.c_char_p, []),
+    "pk_last_error": (C.c_char_p, []),
+    "pk_init": (I, []),
+    "pk_device_arch": (I, [I, C.c_char_p, I]),
+    "pk_parse_gcn_arch_name": (I, [C.c_char_p, C.c_char_p, I]),
+    "launch_rmsnorm": (I, [P, P, P, I, I, F, P]),
+    "launch_gelu": (I, [P, P, I, P]),
+    "launch_matmul": (I, [P, P, P, I, I, I, P]),
+    "launch_softmax": (I, [P, P, I, I, P]),
+    "launch_fused_rmsnorm_matmul": (I, [P, P, P, I, I, I, F, P]),
+    "launch_fused_matmul_bias_gelu": (I, [P, P, P, P, I, I, I, P]),
+    "launch_attention_prefill": (I, [P, P, P, P, I, I, I, I, I, F, I, P]),
+    "launch_kv_cache_update": (I, [P, P, P, I, I, I, I, I, P]),
+    "launch_matmul_int8": (I, [P, P, P, P, I, I, I, P]),
+    "launch_fused_residual_rmsnorm": (I, [P, P, P, P, I, I, F, P]),
+    "launch_fused_softmax_mask": (I, [P, P, P, I, I, P]),
+    "launch_fused_rmsnorm_matmul_gamma": (I, [P, P, P, P, I, I, I, F, P]),
+    "launch_fused_matmul_bias_residual": (I, [P, P, P, P, P, I, I, I, P]),
+    "launch_fused_kv_append_attention": (I, [P, P, P, P, P, P, I, I, I, I, I, I, F, I, P]),
+    "launch_quantize_int8_per_channel": (I, [P, P, P, I, I, P]),
+    "pk_mlp_block_workspace_size": (SZ, [I, I, I]),
+    "launch_mlp_block": (I, [P, P, P, P, P, P, P, I, I, I, F, P, SZ, P]),
+    "pk_decode_mlp_int8_workspace_size": (SZ, [I, I, I]),
+    "launch_decode_mlp_int8": (I, [P, P, P, P, P, P, I, I, I, P, SZ, P]),
+    "pk_gemm_ex": (I, [I, P, P, P, P, P, I, I, I, I, P]),
+    "pk_synth_normal_bf16": (None, [U64, U64, D, D, P, I64]),
+    "pk_synth_normal_f32": (None, [U64, U64, D, D, P, I64]),
+    "pk_synth_mask_bf16": (None, [U64, U64, D, P, I64]),
+}
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load the in-tree library (built by polykernel_amd.build / __graft_entry__.build)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m polykernel_amd.build` "
+            "(the kernels have no CPU fallback)"
+        )
+    lib = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().pk_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, name: str) -> None:
+    if rc != PK_OK:
+        raise PolyKernelError(name, rc, last_error())

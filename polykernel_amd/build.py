@@ -1,0 +1,72 @@
+"""Build the gfx950 kernel library in-tree.
+
+    python -m polykernel_amd.build          # -> polykernel_amd/libpolykernel_amd.so
+
+Every csrc/*.hip file is compiled by hipcc for gfx950 only (no CUDA, no other
+targets) and linked into one shared library whose exported symbols are the
+C-ABI of include/polykernel_amd.h.  Packed-fp32 instruction selection is turned
+off (-packed-fp32-ops); fp32 division and square root keep HIP's correctly
+rounded defaults (no fast-math).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+OBJ = PKG / "_build"
+LIB = PKG / "libpolykernel_amd.so"
+ARCH = "gfx950"
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+    "-I", str(PKG.parent / "include"),
+]
+
+
+def _compile(src: Path) -> Path:
+    out = OBJ / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        msg = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{msg}")
+    return out
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every kernel source and link libpolykernel_amd.so (always rebuilds)."""
+    OBJ.mkdir(exist_ok=True)
+    srcs = sorted(CSRC.glob("*.hip"))
+    if not srcs:
+        raise RuntimeError(f"no sources under {CSRC}")
+    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"[polykernel_amd] built {LIB} from {len(srcs)} sources", flush=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

@@ -1,0 +1,235 @@
+// core.hip -- library state behind the C-ABI: error messages, per-device GELU
+// table, library-owned workspace, device/arch detection, synthetic inputs.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "pk_common.hpp"
+
+namespace pk {
+
+namespace {
+thread_local char g_err[512] = "";
+constexpr int kMaxDevices = 64;
+
+std::mutex g_mu;
+bool g_table_ready[kMaxDevices] = {};
+const uint16_t *g_table_ptr[kMaxDevices] = {};
+void *g_ws_ptr[kMaxDevices] = {};
+size_t g_ws_bytes[kMaxDevices] = {};
+}  // namespace
+
+void set_error(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+int hip_fail(hipError_t e, const char *what) {
+  set_error("%s failed: %s", what, hipGetErrorString(e));
+  return e == hipErrorNoDevice ? PK_ERR_NO_DEVICE : PK_ERR_HIP;
+}
+
+// GELU over every bf16 code, following kernels/cpu/cpu_reference.cpp:46-55:
+// e = (float)erf((double)(x * 0.70710678f)); y = bf16((0.5f * x) * (1.0f + e)).
+// NaN codes map to their quiet form and -inf to the x86 default NaN (0xFFC0),
+// which is what that host arithmetic produces for those inputs.
+__device__ uint16_t g_gelu_table_storage[65536];
+
+__global__ void gelu_table_init_kernel(uint16_t *tab) {
+#pragma clang fp contract(off)
+  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= 65536u) return;
+  const uint32_t exp_bits = b & 0x7F80u, man = b & 0x007Fu;
+  if (exp_bits == 0x7F80u && man != 0u) {
+    tab[b] = (uint16_t)(b | 0x0040u);
+    return;
+  }
+  if (b == 0xFF80u) {
+    tab[b] = 0xFFC0u;
+    return;
+  }
+  const float kInvSqrt2 = 0.70710678118654752440f;
+  const float x = bf2f(b);
+  const float e = (float)erf((double)(x * kInvSqrt2));
+  const float y = (0.5f * x) * (1.0f + e);
+  tab[b] = (uint16_t)f2bf(y);
+}
+
+int gelu_table(const uint16_t **table) {
+  int dev = 0;
+  PK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("device ordinal %d out of range", dev);
+    return PK_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_table_ready[dev]) {
+    void *p = nullptr;
+    PK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_gelu_table_storage)));
+    uint16_t *tab = static_cast<uint16_t *>(p);
+    gelu_table_init_kernel<<<256, 256, 0, nullptr>>>(tab);
+    PK_LAUNCH_CHECK("gelu_table_init_kernel");
+    // One-time set-up: make the table visible to every stream before use.
+    PK_HIP(hipDeviceSynchronize());
+    g_table_ptr[dev] = tab;
+    g_table_ready[dev] = true;
+  }
+  *table = g_table_ptr[dev];
+  return PK_OK;
+}
+
+int library_workspace(size_t bytes, void **ptr) {
+  int dev = 0;
+  PK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("device ordinal %d out of range", dev);
+    return PK_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_ws_bytes[dev] < bytes) {
+    if (g_ws_ptr[dev]) {
+      // Earlier launches may still read the old buffer.
+      PK_HIP(hipDeviceSynchronize());
+      PK_HIP(hipFree(g_ws_ptr[dev]));
+      g_ws_ptr[dev] = nullptr;
+      g_ws_bytes[dev] = 0;
+    }
+    size_t want = std::max<size_t>(bytes, size_t(1) << 20);
+    PK_HIP(hipMalloc(&g_ws_ptr[dev], want));
+    g_ws_bytes[dev] = want;
+  }
+  *ptr = g_ws_ptr[dev];
+  return PK_OK;
+}
+
+// ---- synthetic generator ---------------------------------------------------
+namespace {
+inline uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+inline uint64_t stream_key(uint64_t seed, uint64_t stream_id) {
+  return splitmix64(seed ^ (stream_id * 0xD1B54A32D192ED03ull));
+}
+
+// Standard normal draw i of a (seed, stream) pair: Box-Muller in double on two
+// 53-bit uniforms; u1 in (0,1], u2 in [0,1).
+inline double normal_at(uint64_t key, int64_t i) {
+  const uint64_t a = splitmix64(key + 2ull * (uint64_t)i);
+  const uint64_t b = splitmix64(key + 2ull * (uint64_t)i + 1ull);
+  const double u1 = (double)((a >> 11) + 1ull) * 0x1.0p-53;
+  const double u2 = (double)(b >> 11) * 0x1.0p-53;
+  return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586476925 * u2);
+}
+
+inline uint16_t host_f2bf(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u)
+    return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename F>
+void parallel_for(int64_t n, F &&f) {
+  unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  int64_t nt = std::min<int64_t>(hw, std::max<int64_t>(1, n / 65536));
+  if (nt <= 1) {
+    f(0, n);
+    return;
+  }
+  std::vector<std::thread> th;
+  int64_t chunk = (n + nt - 1) / nt;
+  for (int64_t t = 0; t < nt; ++t) {
+    int64_t lo = t * chunk, hi = std::min(n, lo + chunk);
+    if (lo >= hi) break;
+    th.emplace_back([=, &f] { f(lo, hi); });
+  }
+  for (auto &x : th) x.join();
+}
+}  // namespace
+
+}  // namespace pk
+
+using namespace pk;
+
+extern "C" {
+
+const char *pk_version(void) { return "polykernel_amd 0.1.0 gfx950"; }
+
+const char *pk_last_error(void) { return g_err; }
+
+int pk_init(void) {
+  const uint16_t *t = nullptr;
+  return gelu_table(&t);
+}
+
+int pk_parse_gcn_arch_name(const char *name, char *buf, int buf_len) {
+  if (!name || !buf || buf_len <= 0) {
+    set_error("pk_parse_gcn_arch_name: null argument");
+    return PK_ERR_INVALID_ARG;
+  }
+  buf[0] = '\0';
+  // Leading "gfx" followed by hex-ish digits/letters up to ':' (e.g. gfx950, gfx90a).
+  if (std::strncmp(name, "gfx", 3) != 0) return PK_OK;
+  int n = 3;
+  while (name[n] && name[n] != ':' &&
+         ((name[n] >= '0' && name[n] <= '9') || (name[n] >= 'a' && name[n] <= 'f')))
+    ++n;
+  if (n == 3) return PK_OK;
+  if (n + 1 > buf_len) {
+    set_error("pk_parse_gcn_arch_name: buffer too small");
+    return PK_ERR_INVALID_ARG;
+  }
+  std::memcpy(buf, name, n);
+  buf[n] = '\0';
+  return PK_OK;
+}
+
+int pk_device_arch(int ordinal, char *buf, int buf_len) {
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, ordinal);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  return pk_parse_gcn_arch_name(p.gcnArchName, buf, buf_len);
+}
+
+void pk_synth_normal_bf16(uint64_t seed, uint64_t stream_id, double mean, double std_dev,
+                          uint16_t *out, int64_t n) {
+  const uint64_t key = stream_key(seed, stream_id);
+  parallel_for(n, [&](int64_t lo, int64_t hi) {
+    for (int64_t i = lo; i < hi; ++i)
+      out[i] = host_f2bf((float)(mean + std_dev * normal_at(key, i)));
+  });
+}
+
+void pk_synth_normal_f32(uint64_t seed, uint64_t stream_id, double mean, double std_dev,
+                         float *out, int64_t n) {
+  const uint64_t key = stream_key(seed, stream_id);
+  parallel_for(n, [&](int64_t lo, int64_t hi) {
+    for (int64_t i = lo; i < hi; ++i) out[i] = (float)(mean + std_dev * normal_at(key, i));
+  });
+}
+
+void pk_synth_mask_bf16(uint64_t seed, uint64_t stream_id, double p, uint16_t *out, int64_t n) {
+  const uint64_t key = stream_key(seed, stream_id);
+  parallel_for(n, [&](int64_t lo, int64_t hi) {
+    for (int64_t i = lo; i < hi; ++i) {
+      const double u = (double)(splitmix64(key + (uint64_t)i) >> 11) * 0x1.0p-53;
+      out[i] = (u < p) ? (uint16_t)0xFF80u : (uint16_t)0x0000u;
+    }
+  });
+}
+
+}  // extern "C"

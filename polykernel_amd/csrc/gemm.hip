@@ -1,0 +1,557 @@
+// gemm.hip -- bf16 MFMA GEMM for gfx950 with fused epilogues.
+//
+// C[M,N] = A[M,K] @ B[K,N] with A K-contiguous and B N-contiguous (the
+// reference layouts, kernels/cpu/cpu_reference.cpp:64-78), fp32 accumulation on
+// v_mfma_f32_32x32x16_bf16.  Per workgroup a BM x BN tile; WM x WN waves, each
+// owning a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks.  A and B k-tiles of
+// 64 are staged through LDS, double-buffered with one barrier per k-tile:
+//   - A rows (128 B) are stored with 16-byte chunks XOR-swizzled by (row & 7),
+//     read as one ds_read_b128 per MFMA A-operand;
+//   - B rows keep the global N-contiguous order (16-byte chunks swizzled by
+//     k), and the MFMA B-operand (8 consecutive k of one column) is assembled
+//     by two ds_read_b64_tr_b16 transpose reads, so no pre-packed weights and
+//     no register transposes are needed.
+// Workgroups are remapped so each XCD gets a contiguous band of tiles, rastered
+// in groups of tile-rows for L2 reuse.
+//
+// Epilogues reproduce the golden per-stage bf16 rounding
+// (tests/golden/golden.py:48-66, kernels/cpu/cpu_reference.cpp:92-105):
+//   EPI_NONE        c = bf16(acc)
+//   EPI_BIAS_GELU   c = gelu(bf16(bf16(acc) + bias[n]))      (GELU by exact table)
+//   EPI_BIAS_RESID  c = bf16(bf16(bf16(acc) + bias[n]) + R[m,n])
+//   EPI_RESID       c = bf16(bf16(acc) + R[m,n])
+#include "pk_common.hpp"
+
+namespace pk {
+
+enum Epi : int { EPI_NONE = 0, EPI_BIAS_GELU = 1, EPI_BIAS_RESID = 2, EPI_RESID = 3 };
+
+struct GemmArgs {
+  const uint16_t *A;
+  const uint16_t *B;
+  uint16_t *C;
+  const uint16_t *bias;
+  const uint16_t *R;
+  const uint16_t *gelu_tab;
+  int M, N, K;
+};
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+constexpr int BK = 64;
+
+// 16-byte-chunk XOR for B rows, chosen so the four rows read by one 16-lane
+// ds_read_b64_tr_b16 group land on distinct LDS banks.
+template <int BN>
+__device__ __forceinline__ int swz_b(int k) {
+  if constexpr (BN >= 128) {
+    constexpr int t[4] = {0, 4, 10, 14};
+    return t[k & 3];
+  } else {
+    return (k & 3) * 2;
+  }
+}
+
+__device__ __forceinline__ bf16x8 lds_read_a(const uint16_t *p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
+}
+
+__device__ __forceinline__ i16x4 lds_read_tr(const uint16_t *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
+}
+
+template <int EPI>
+__device__ __forceinline__ uint16_t epilogue(float acc, int m, int n, const GemmArgs &g,
+                                             float bias_n) {
+#pragma clang fp contract(off)
+  const float t = bf2f(f2bf(acc));
+  if constexpr (EPI == EPI_NONE) {
+    return (uint16_t)f2bf(acc);
+  } else if constexpr (EPI == EPI_BIAS_GELU) {
+    const uint32_t u = f2bf(t + bias_n);
+    return g.gelu_tab[u];
+  } else if constexpr (EPI == EPI_BIAS_RESID) {
+    const float u = bf2f(f2bf(t + bias_n));
+    return (uint16_t)f2bf(u + bf2f(g.R[(size_t)m * g.N + n]));
+  } else {
+    return (uint16_t)f2bf(t + bf2f(g.R[(size_t)m * g.N + n]));
+  }
+}
+
+// Map the linear block id to (tile_m, tile_n): contiguous per-XCD bands
+// (blocks are dispatched round-robin over the 8 XCDs), then grouped raster.
+__device__ __forceinline__ void tile_coords(int bid, int tm, int tn, int &mt, int &nt) {
+  const int total = tm * tn;
+  int b = bid;
+  if ((total & 7) == 0) b = (bid & 7) * (total >> 3) + (bid >> 3);
+  constexpr int GM = 8;
+  const int group = b / (GM * tn);
+  const int first_m = group * GM;
+  const int gsize = min(tm - first_m, GM);
+  const int in_group = b - group * GM * tn;
+  mt = first_m + in_group % gsize;
+  nt = in_group / gsize;
+}
+
+// ---------------------------------------------------------------------------
+// Main GEMM kernel.  ALIGNED: K % 8 == 0, N % 8 == 0 and 16-byte aligned A/B,
+// so every 16-byte chunk is entirely in or out of bounds.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, int EPI, bool ALIGNED>
+__global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int A_CHUNKS = BM * BK / 8, B_CHUNKS = BK * BN / 8;
+  constexpr int AC = A_CHUNKS / NT, BC = B_CHUNKS / NT;
+  static_assert(A_CHUNKS % NT == 0 && B_CHUNKS % NT == 0, "tile/thread mismatch");
+  static_assert(FM >= 1 && FN >= 1, "sub-tile smaller than one MFMA block");
+  constexpr int BROW_CHUNKS = BN / 8;
+
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BK * BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / WN, wn = wid % WN;
+  const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  int mt, nt;
+  tile_coords(blockIdx.x, tm, tn, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int KT = (g.K + BK - 1) / BK;
+
+  u32x4 ra[AC], rb[BC];
+
+  auto load_tiles = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < AC; ++i) {
+      const int q = tid + i * NT, row = q >> 3, c = q & 7;
+      const int gm = m0 + row, gk = k0 + c * 8;
+      if constexpr (ALIGNED) {
+        ra[i] = (gm < g.M && gk < g.K)
+                    ? *reinterpret_cast<const u32x4 *>(g.A + (size_t)gm * g.K + gk)
+                    : u32x4{0, 0, 0, 0};
+      } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = (gm < g.M && gk + 2 * e < g.K) ? g.A[(size_t)gm * g.K + gk + 2 * e] : 0u;
+          const uint32_t hi =
+              (gm < g.M && gk + 2 * e + 1 < g.K) ? g.A[(size_t)gm * g.K + gk + 2 * e + 1] : 0u;
+          w[e] = lo | (hi << 16);
+        }
+        ra[i] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BC; ++i) {
+      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
+      const int gk = k0 + row, gn = n0 + c * 8;
+      if constexpr (ALIGNED) {
+        rb[i] = (gk < g.K && gn < g.N)
+                    ? *reinterpret_cast<const u32x4 *>(g.B + (size_t)gk * g.N + gn)
+                    : u32x4{0, 0, 0, 0};
+      } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = (gk < g.K && gn + 2 * e < g.N) ? g.B[(size_t)gk * g.N + gn + 2 * e] : 0u;
+          const uint32_t hi =
+              (gk < g.K && gn + 2 * e + 1 < g.N) ? g.B[(size_t)gk * g.N + gn + 2 * e + 1] : 0u;
+          w[e] = lo | (hi << 16);
+        }
+        rb[i] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    }
+  };
+
+  auto store_tiles = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < AC; ++i) {
+      const int q = tid + i * NT, row = q >> 3, c = q & 7;
+      *reinterpret_cast<u32x4 *>(&As[s][row * BK + ((c ^ (row & 7)) << 3)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BC; ++i) {
+      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
+      *reinterpret_cast<u32x4 *>(&Bs[s][row * BN + ((c ^ swz_b<BN>(row)) << 3)]) = rb[i];
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Per-lane LDS offsets (elements) that do not depend on the k-substep.
+  const int a_row0 = wm * TM + (lane & 31);
+  const int a_half = lane >> 5;
+  const int grp = lane >> 4, gi = lane & 15;
+  const int b_krow = 8 * (grp >> 1) + (gi >> 2);        // + 16*s + 4*r
+  const int b_col0 = wn * TN + 16 * (grp & 1) + 4 * (gi & 3);  // + 32*fn
+
+  load_tiles(0);
+  store_tiles(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) load_tiles(kt + 1);
+    const uint16_t *as = As[cur];
+    const uint16_t *bs = Bs[cur];
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int row = a_row0 + fm * 32;
+        const int c = 2 * s + a_half;
+        af[fm] = lds_read_a(as + row * BK + ((c ^ (row & 7)) << 3));
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        i16x4 h[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int k = 16 * s + 4 * r + b_krow;
+          const int col = b_col0 + 32 * fn;
+          const int c = col >> 3;
+          h[r] = lds_read_tr(bs + k * BN + ((c ^ swz_b<BN>(k)) << 3) + (col & 7));
+        }
+        short tmp[8] = {h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+        bfr[fn] = __builtin_bit_cast(bf16x8, tmp);
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fm][fn] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[fm], bfr[fn], acc[fm][fn], 0, 0, 0);
+    }
+    if (kt + 1 < KT) store_tiles(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: acc[fm][fn][i] -> row (i/4)*8 + (lane/32)*4 + i%4, col lane%32.
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int n = n0 + wn * TN + fn * 32 + (lane & 31);
+    const bool nok = n < g.N;
+    float bias_n = 0.f;
+    if constexpr (EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID)
+      bias_n = (nok && g.bias) ? bf2f(g.bias[n]) : 0.f;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = m0 + wm * TM + fm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+        if (nok && m < g.M) g.C[(size_t)m * g.N + n] = epilogue<EPI>(acc[fm][fn][i], m, n, g, bias_n);
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int EPI>
+int launch_tile(const GemmArgs &g, bool aligned, hipStream_t st) {
+  const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+  if (aligned)
+    gemm_kernel<BM, BN, WM, WN, EPI, true><<<tiles, WM * WN * 64, 0, st>>>(g);
+  else
+    gemm_kernel<BM, BN, WM, WN, EPI, false><<<tiles, WM * WN * 64, 0, st>>>(g);
+  PK_LAUNCH_CHECK("gemm_kernel");
+  return PK_OK;
+}
+
+template <int EPI>
+int gemm_dispatch(const GemmArgs &g, int tile, hipStream_t st) {
+  const bool aligned = (g.K % 8 == 0) && (g.N % 8 == 0) && aligned16(g.A) && aligned16(g.B);
+  switch (tile) {
+    case 0: return launch_tile<256, 256, 2, 4, EPI>(g, aligned, st);
+    case 1: return launch_tile<128, 128, 2, 2, EPI>(g, aligned, st);
+    default: return launch_tile<64, 64, 2, 2, EPI>(g, aligned, st);
+  }
+}
+
+// Largest tile that still gives at least ~one workgroup per CU.
+int pick_tile(int M, int N) {
+  const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
+  const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+  if (t256 >= 200) return 0;
+  if (t128 >= 200) return 1;
+  return 2;
+}
+
+}  // namespace
+
+int gemm_run(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
+             const uint16_t *R, int M, int N, int K, hipStream_t st, int tile = -1) {
+  GemmArgs g{A, B, C, bias, R, nullptr, M, N, K};
+  if (epi == EPI_BIAS_GELU) {
+    int rc = gelu_table(&g.gelu_tab);
+    if (rc) return rc;
+  }
+  if (tile < 0) tile = pick_tile(M, N);
+  switch (epi) {
+    case EPI_NONE: return gemm_dispatch<EPI_NONE>(g, tile, st);
+    case EPI_BIAS_GELU: return gemm_dispatch<EPI_BIAS_GELU>(g, tile, st);
+    case EPI_BIAS_RESID: return gemm_dispatch<EPI_BIAS_RESID>(g, tile, st);
+    default: return gemm_dispatch<EPI_RESID>(g, tile, st);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm -> MatMul with the normalised A row-panel resident in LDS
+// (short K: 32 x K bf16 <= 96 KiB).  The block first computes its 32 row RMS
+// values, writes bf16((x / rms) * gamma) into LDS once (exact fp32 division,
+// kernels/cpu/cpu_reference.cpp:16-44), then streams B k-tiles (double
+// buffered) through the same MFMA loop as gemm_kernel.
+// ---------------------------------------------------------------------------
+constexpr int RP_BM = 32, RP_BN = 64, RP_WAVES = 2;
+constexpr int RP_MAX_K = 1536;
+
+__global__ __launch_bounds__(RP_WAVES * 64) void rmsnorm_panel_gemm_kernel(
+    const uint16_t *__restrict__ X, const uint16_t *__restrict__ gamma,
+    const uint16_t *__restrict__ B, uint16_t *__restrict__ C, int M, int N, int K, float inv_cols,
+    float eps) {
+#pragma clang fp contract(off)
+  constexpr int NT = RP_WAVES * 64;
+  constexpr int BN = RP_BN;
+  constexpr int B_CHUNKS = BK * BN / 8, BC = B_CHUNKS / NT;
+  constexpr int BROW_CHUNKS = BN / 8;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t *Ap = smem;                       // [32][K]
+  uint16_t *Bs0 = smem + RP_BM * K;          // [2][BK*BN]
+  __shared__ float rms_s[RP_BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tn = (N + BN - 1) / BN;
+  const int mt = blockIdx.x / tn, nt = blockIdx.x % tn;
+  const int m0 = mt * RP_BM, n0 = nt * BN;
+  const int kchunks = K >> 3;
+
+  // Row statistics: each wave reduces 16 rows.
+  for (int r = wid; r < RP_BM; r += RP_WAVES) {
+    const int gm = m0 + r;
+    float ss = 0.f;
+    if (gm < M) {
+      for (int c = lane; c < kchunks; c += 64) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = lo_bf(v[e]), b = hi_bf(v[e]);
+          ss += a * a;
+          ss += b * b;
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) rms_s[r] = sqrtf(ss * inv_cols + eps);
+  }
+  __syncthreads();
+  // Normalise the panel into LDS (16-byte chunks swizzled by row within each
+  // aligned group of 8 chunks).
+  for (int q = tid; q < RP_BM * kchunks; q += NT) {
+    const int r = q / kchunks, c = q % kchunks;
+    const int gm = m0 + r;
+    u32x4 o = {0, 0, 0, 0};
+    if (gm < M) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
+      u32x4 gv = {0, 0, 0, 0};
+      if (gamma) gv = *reinterpret_cast<const u32x4 *>(gamma + c * 8);
+      const float rms = rms_s[r];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a = lo_bf(v[e]) / rms, b = hi_bf(v[e]) / rms;
+        if (gamma) {
+          a *= lo_bf(gv[e]);
+          b *= hi_bf(gv[e]);
+        }
+        o[e] = pack_bf(a, b);
+      }
+    }
+    *reinterpret_cast<u32x4 *>(Ap + r * K + ((c ^ (r & 7)) << 3)) = o;
+  }
+
+  u32x4 rb[BC];
+  auto load_b = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < BC; ++i) {
+      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
+      const int gk = k0 + row, gn = n0 + c * 8;
+      rb[i] = (gk < K && gn < N) ? *reinterpret_cast<const u32x4 *>(B + (size_t)gk * N + gn)
+                                 : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_b = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < BC; ++i) {
+      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
+      *reinterpret_cast<u32x4 *>(&Bs0[s * BK * BN + row * BN + ((c ^ swz_b<BN>(row)) << 3)]) = rb[i];
+    }
+  };
+
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  const int KT = K / BK;
+  const int grp = lane >> 4, gi = lane & 15;
+  const int b_krow = 8 * (grp >> 1) + (gi >> 2);
+  const int b_col = wid * 32 + 16 * (grp & 1) + 4 * (gi & 3);
+  const int a_row = lane & 31;
+
+  load_b(0);
+  store_b(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) load_b(kt + 1);
+    const uint16_t *bs = Bs0 + cur * BK * BN;
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int c = kt * 8 + 2 * s + (lane >> 5);
+      const bf16x8 af = lds_read_a(Ap + a_row * K + ((c ^ (a_row & 7)) << 3));
+      i16x4 h[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int k = 16 * s + 4 * r + b_krow;
+        const int cc = b_col >> 3;
+        h[r] = lds_read_tr(bs + k * BN + ((cc ^ swz_b<BN>(k)) << 3) + (b_col & 7));
+      }
+      short tmp[8] = {h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8, tmp), acc, 0,
+                                                     0, 0);
+    }
+    if (kt + 1 < KT) store_b(cur ^ 1);
+    __syncthreads();
+  }
+  const int n = n0 + wid * 32 + (lane & 31);
+  if (n < N) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int m = m0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+      if (m < M) C[(size_t)m * N + n] = (uint16_t)f2bf(acc[i]);
+    }
+  }
+}
+
+int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, int rows, int cols,
+                   float eps, hipStream_t st);
+
+int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_t *W, uint16_t *out,
+                         int M, int N, int K, float eps, hipStream_t st, const char *name) {
+  PK_CHECK_ARG(x && W && out, "%s: null tensor pointer", name);
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "%s: invalid shape M=%d N=%d K=%d", name, M, N, K);
+  if (M == 0 || N == 0) return PK_OK;
+  const bool panel_ok = (K % BK == 0) && K <= RP_MAX_K && (N % 8 == 0) && aligned16(x) &&
+                        aligned16(W) && (!gamma || aligned16(gamma));
+  if (panel_ok) {
+    const int tiles = ((M + RP_BM - 1) / RP_BM) * ((N + RP_BN - 1) / RP_BN);
+    const size_t lds = (size_t)RP_BM * K * 2 + 2 * BK * RP_BN * 2;
+    rmsnorm_panel_gemm_kernel<<<tiles, RP_WAVES * 64, lds, st>>>(x, gamma, W, out, M, N, K,
+                                                                 1.0f / (float)K, eps);
+    PK_LAUNCH_CHECK(name);
+    return PK_OK;
+  }
+  // Long rows: normalise once into library workspace, then the plain GEMM.
+  void *ws = nullptr;
+  int rc = library_workspace((size_t)M * K * 2, &ws);
+  if (rc) return rc;
+  uint16_t *a = static_cast<uint16_t *>(ws);
+  rc = rmsnorm_launch(x, gamma, a, M, K, eps, st);
+  if (rc) return rc;
+  return gemm_run(EPI_NONE, a, W, out, nullptr, nullptr, M, N, K, st);
+}
+
+}  // namespace pk
+
+using namespace pk;
+
+extern "C" {
+
+int launch_matmul(const uint16_t *A, const uint16_t *B, uint16_t *C, int M, int N, int K,
+                  void *stream) {
+  PK_CHECK_ARG(A && B && C, "launch_matmul: null tensor pointer");
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "launch_matmul: invalid shape");
+  if (M == 0 || N == 0) return PK_OK;
+  PK_CHECK_ARG(K > 0, "launch_matmul: K must be positive");
+  return gemm_run(EPI_NONE, A, B, C, nullptr, nullptr, M, N, K, (hipStream_t)stream);
+}
+
+int launch_fused_matmul_bias_gelu(const uint16_t *a, const uint16_t *b, const uint16_t *bias,
+                                  uint16_t *output, int M, int N, int K, void *stream) {
+  PK_CHECK_ARG(a && b && bias && output, "launch_fused_matmul_bias_gelu: null tensor pointer");
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "launch_fused_matmul_bias_gelu: invalid shape");
+  if (M == 0 || N == 0) return PK_OK;
+  return gemm_run(EPI_BIAS_GELU, a, b, output, bias, nullptr, M, N, K, (hipStream_t)stream);
+}
+
+int launch_fused_matmul_bias_residual(const uint16_t *a, const uint16_t *b, const uint16_t *bias,
+                                      const uint16_t *residual, uint16_t *out, int M, int N, int K,
+                                      void *stream) {
+  PK_CHECK_ARG(a && b && residual && out, "launch_fused_matmul_bias_residual: null tensor pointer");
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "launch_fused_matmul_bias_residual: invalid shape");
+  if (M == 0 || N == 0) return PK_OK;
+  return gemm_run(bias ? EPI_BIAS_RESID : EPI_RESID, a, b, out, bias, residual, M, N, K,
+                  (hipStream_t)stream);
+}
+
+int launch_fused_rmsnorm_matmul(const uint16_t *input, const uint16_t *weight, uint16_t *output,
+                                int M, int N, int K, float eps, void *stream) {
+  return fused_rmsnorm_matmul(input, nullptr, weight, output, M, N, K, eps, (hipStream_t)stream,
+                              "launch_fused_rmsnorm_matmul");
+}
+
+int launch_fused_rmsnorm_matmul_gamma(const uint16_t *x, const uint16_t *gamma, const uint16_t *W,
+                                      uint16_t *out, int M, int N, int K, float eps, void *stream) {
+  return fused_rmsnorm_matmul(x, gamma, W, out, M, N, K, eps, (hipStream_t)stream,
+                              "launch_fused_rmsnorm_matmul_gamma");
+}
+
+size_t pk_mlp_block_workspace_size(int M, int d, int F) {
+  auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
+  return up((size_t)M * d * 2) + up((size_t)M * F * 2);
+}
+
+int launch_mlp_block(const uint16_t *x, const uint16_t *gamma, const uint16_t *W1,
+                     const uint16_t *b1, const uint16_t *W2, const uint16_t *b2, uint16_t *out,
+                     int M, int d, int F, float eps, void *workspace, size_t workspace_bytes,
+                     void *stream) {
+  PK_CHECK_ARG(x && W1 && b1 && W2 && b2 && out, "launch_mlp_block: null tensor pointer");
+  PK_CHECK_ARG(M >= 0 && d > 0 && F > 0, "launch_mlp_block: invalid shape");
+  if (M == 0) return PK_OK;
+  const size_t need = pk_mlp_block_workspace_size(M, d, F);
+  if (!workspace || workspace_bytes < need) {
+    set_error("launch_mlp_block: workspace of %zu bytes required, got %zu", need, workspace_bytes);
+    return PK_ERR_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  uint16_t *a = static_cast<uint16_t *>(workspace);
+  uint16_t *h = a + (((size_t)M * d * 2 + 255) & ~size_t(255)) / 2;
+  int rc = rmsnorm_launch(x, gamma, a, M, d, eps, st);
+  if (rc) return rc;
+  rc = gemm_run(EPI_BIAS_GELU, a, W1, h, b1, nullptr, M, F, d, st);
+  if (rc) return rc;
+  return gemm_run(EPI_BIAS_RESID, h, W2, out, b2, x, M, d, F, st);
+}
+
+// Test/tuning hook: run one GEMM epilogue variant with an explicit tile choice
+// (0: 256x256, 1: 128x128, 2: 64x64; -1: heuristic).
+int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
+               const uint16_t *R, int M, int N, int K, int tile, void *stream) {
+  PK_CHECK_ARG(A && B && C, "pk_gemm_ex: null tensor pointer");
+  PK_CHECK_ARG(M > 0 && N > 0 && K > 0, "pk_gemm_ex: invalid shape");
+  PK_CHECK_ARG(epi >= 0 && epi <= 3 && tile >= -1 && tile <= 2, "pk_gemm_ex: bad epi/tile");
+  return gemm_run(epi, A, B, C, bias, R, M, N, K, (hipStream_t)stream, tile);
+}
+
+}  // extern "C"

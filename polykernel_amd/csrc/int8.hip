@@ -1,0 +1,318 @@
+// int8.hip -- int8 weight-only matmul for decode shapes (small M) on gfx950.
+//
+// C[M,N] = bf16(scale[n] * sum_k A[m,k] * Wq[k,n]), A bf16 [M,K], Wq int8 [K,N]
+// (N contiguous, the reference layout of kernels/generated/matmul_int8.cu:47-88).
+// The per-channel scale is applied once to the fp32 dot product instead of to
+// every weight (kernels/cpu/matmul_quant.cpp:189-199 dequantises per element);
+// int8 values and their products with bf16 activations are exact in fp32, so
+// only the summation order and that one rounding differ.
+//
+// Streaming design (HBM-bound: every weight byte is read once):
+//   - a workgroup owns a 64-column slice of N and a K range (split-K);
+//   - each of its 4 waves streams a quarter of that K range in 32-row steps:
+//     two 16-byte loads per lane fetch a 32x64 int8 block, which is widened to
+//     bf16 in registers (exact) and written to the wave's private LDS block in
+//     the swizzled N-contiguous layout of the bf16 GEMM;
+//   - ds_read_b64_tr_b16 assembles the MFMA B operand (8 consecutive k of one
+//     column); A (16 rows of activations) is read straight from global/L2;
+//   - v_mfma_f32_16x16x32_bf16, 4 column blocks per step;
+//   - the 4 waves' accumulators are summed in LDS in a fixed order; with one
+//     K split the epilogue runs in place, otherwise fp32 partials go to a
+//     workspace and int8_reduce_kernel sums the splits in split order.
+// Epilogues: plain, GELU (exact table) and residual add, each with the
+// golden's per-stage bf16 rounding.
+#include "pk_common.hpp"
+
+namespace pk {
+
+enum Int8Epi : int { I8_NONE = 0, I8_GELU = 1, I8_RESID = 2 };
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+constexpr int I8_BN = 64;      // columns per workgroup
+constexpr int I8_STEP = 32;    // k rows per wave step
+constexpr int I8_WAVES = 4;
+constexpr int I8_THREADS = I8_WAVES * 64;
+
+struct Int8Args {
+  const uint16_t *A;
+  const int8_t *W;
+  const float *scale;
+  float *partial;  // [splits][M][N] when splits > 1
+  uint16_t *C;
+  const uint16_t *R;
+  const uint16_t *gelu_tab;
+  int M, N, K;
+  int splits;
+  int kper;  // rows of K per split (multiple of I8_STEP * I8_WAVES)
+};
+
+__device__ __forceinline__ int swz64(int k) { return (k & 3) * 2; }
+
+// Widen 4 int8 (one dword) to 4 bf16 in two dwords.  int8 -> fp32 is exact and
+// the fp32 value has at most 8 significant bits, so its top half is the bf16.
+__device__ __forceinline__ void widen4(uint32_t w, uint32_t &lo, uint32_t &hi) {
+  const float f0 = (float)(int8_t)(w & 0xFF), f1 = (float)(int8_t)((w >> 8) & 0xFF);
+  const float f2 = (float)(int8_t)((w >> 16) & 0xFF), f3 = (float)(int8_t)(w >> 24);
+  lo = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+  hi = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xFFFF0000u);
+}
+
+template <int EPI>
+__device__ __forceinline__ uint16_t int8_epilogue(float dot, int m, int n, const Int8Args &g) {
+#pragma clang fp contract(off)
+  const uint32_t t = f2bf(dot * g.scale[n]);
+  if constexpr (EPI == I8_NONE) {
+    return (uint16_t)t;
+  } else if constexpr (EPI == I8_GELU) {
+    return g.gelu_tab[t];
+  } else {
+    return (uint16_t)f2bf(bf2f(t) + bf2f(g.R[(size_t)m * g.N + n]));
+  }
+}
+
+template <bool ALIGNED, int EPI>
+__global__ __launch_bounds__(I8_THREADS) void int8_gemm_kernel(Int8Args g) {
+  __shared__ __attribute__((aligned(16))) uint16_t wlds[I8_WAVES][I8_STEP * I8_BN];
+  __shared__ float red[I8_WAVES][16 * I8_BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int n0 = blockIdx.x * I8_BN;
+  const int split = blockIdx.y;
+  const int m0 = blockIdx.z * 16;
+  const int kb0 = split * g.kper;
+  const int kb1 = min(g.K, kb0 + g.kper);
+  const int wk = g.kper / I8_WAVES;  // rows per wave
+  const int kw0 = kb0 + wid * wk;
+  const int kw1 = min(kb1, kw0 + wk);
+
+  uint16_t *my = wlds[wid];
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // A operand (16x16x32): row m = lane % 16, k = 8 * (lane / 16) + 0..7.
+  const int am = m0 + (lane & 15);
+  const int ak = 8 * (lane >> 4);
+  // W block loads: part p covers rows p*16 + lane/4, columns (lane%4)*16 .. +15.
+  const int wr = lane >> 2, wc = (lane & 3) * 16;
+  // tr-read coordinates (per 16-lane group g: k base 8g; lane i -> row i/4, col 4*(i%4)).
+  const int grp = lane >> 4, gi = lane & 15;
+
+  for (int k0 = kw0; k0 < kw1; k0 += I8_STEP) {
+    // ---- loads
+    u32x4 wv[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int k = k0 + p * 16 + wr;
+      const int n = n0 + wc;
+      if constexpr (ALIGNED) {
+        wv[p] = (k < kw1 && n < g.N) ? *reinterpret_cast<const u32x4 *>(g.W + (size_t)k * g.N + n)
+                                     : u32x4{0, 0, 0, 0};
+      } else {
+        uint32_t w4[4] = {0, 0, 0, 0};
+        if (k < kw1) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (n + e < g.N)
+              w4[e >> 2] |= ((uint32_t)(uint8_t)g.W[(size_t)k * g.N + n + e]) << (8 * (e & 3));
+        }
+        wv[p] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+      }
+    }
+    u32x4 av;
+    {
+      const int k = k0 + ak;
+      if constexpr (ALIGNED) {
+        av = (am < g.M && k < kw1) ? *reinterpret_cast<const u32x4 *>(g.A + (size_t)am * g.K + k)
+                                   : u32x4{0, 0, 0, 0};
+      } else {
+        uint32_t a4[4] = {0, 0, 0, 0};
+        if (am < g.M) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k + e < kw1) a4[e >> 1] |= (uint32_t)g.A[(size_t)am * g.K + k + e] << (16 * (e & 1));
+        }
+        av = u32x4{a4[0], a4[1], a4[2], a4[3]};
+      }
+    }
+    // ---- widen to bf16 and stage in this wave's LDS block
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int row = p * 16 + wr;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t o0, o1, o2, o3;
+        widen4(wv[p][2 * h], o0, o1);
+        widen4(wv[p][2 * h + 1], o2, o3);
+        const u32x4 o = {o0, o1, o2, o3};
+        const int c = (wc >> 3) + h;  // 16-byte chunk of the 128-byte row
+        *reinterpret_cast<u32x4 *>(my + row * I8_BN + ((c ^ swz64(row)) << 3)) = o;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bf16x8 a = __builtin_bit_cast(bf16x8, av);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      i16x4 h[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int row = 8 * grp + 4 * r + (gi >> 2);
+        const int col = nb * 16 + 4 * (gi & 3);
+        const int c = col >> 3;
+        h[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4 *)(my + row * I8_BN + ((c ^ swz64(row)) << 3) + (col & 7)));
+      }
+      short tmp[8] = {h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+      acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, tmp), acc[nb],
+                                                        0, 0, 0);
+    }
+    // The next step overwrites this wave's block: keep its reads ahead of those writes.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---- cross-wave reduction (fixed order) -> epilogue or partial
+  // D layout (16x16): acc[nb][i] -> row (lane/16)*4 + i, col nb*16 + lane%16.
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wid][((lane >> 4) * 4 + i) * I8_BN + nb * 16 + (lane & 15)] = acc[nb][i];
+  __syncthreads();
+  for (int e = tid; e < 16 * I8_BN; e += I8_THREADS) {
+    const int r = e / I8_BN, c = e % I8_BN;
+    const int m = m0 + r, n = n0 + c;
+    if (m >= g.M || n >= g.N) continue;
+    float s = red[0][e];
+#pragma unroll
+    for (int w = 1; w < I8_WAVES; ++w) s += red[w][e];
+    if (g.splits > 1)
+      g.partial[((size_t)split * g.M + m) * g.N + n] = s;
+    else
+      g.C[(size_t)m * g.N + n] = int8_epilogue<EPI>(s, m, n, g);
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void int8_reduce_kernel(Int8Args g) {
+  const int64_t total = (int64_t)g.M * g.N;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+    float s = g.partial[t];
+    for (int sp = 1; sp < g.splits; ++sp) s += g.partial[(size_t)sp * total + t];
+    const int m = (int)(t / g.N), n = (int)(t % g.N);
+    g.C[t] = int8_epilogue<EPI>(s, m, n, g);
+  }
+}
+
+// Number of K splits: enough workgroups to cover the chip ~4x, each wave
+// keeping at least 8 steps.
+int choose_splits(int M, int N, int K) {
+  const int tiles = ((N + I8_BN - 1) / I8_BN) * ((M + 15) / 16);
+  const int unit = I8_STEP * I8_WAVES;
+  const int kunits = (K + unit - 1) / unit;
+  int s = 1;
+  while (tiles * s < 1024 && kunits / (2 * s) >= 2) s *= 2;
+  return s;
+}
+
+}  // namespace
+
+size_t int8_workspace_bytes(int M, int N, int K) {
+  const int s = choose_splits(M, N, K);
+  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+}
+
+int int8_run(int epi, const uint16_t *A, const int8_t *W, const float *scale, uint16_t *C,
+             const uint16_t *R, int M, int N, int K, void *ws, size_t ws_bytes, hipStream_t st) {
+  Int8Args g{A, W, scale, nullptr, C, R, nullptr, M, N, K, 1, 0};
+  if (epi == I8_GELU) {
+    int rc = gelu_table(&g.gelu_tab);
+    if (rc) return rc;
+  }
+  g.splits = choose_splits(M, N, K);
+  const int unit = I8_STEP * I8_WAVES;
+  g.kper = ((K + g.splits - 1) / g.splits + unit - 1) / unit * unit;
+  g.splits = (K + g.kper - 1) / g.kper;
+  if (g.splits > 1) {
+    const size_t need = (size_t)g.splits * M * N * sizeof(float);
+    if (ws == nullptr) {
+      int rc = library_workspace(need, &ws);
+      if (rc) return rc;
+    } else if (ws_bytes < need) {
+      set_error("int8 matmul: workspace of %zu bytes required, got %zu", need, ws_bytes);
+      return PK_ERR_WORKSPACE;
+    }
+    g.partial = static_cast<float *>(ws);
+  }
+  const bool aligned = (N % 16 == 0) && (K % 8 == 0) && aligned16(A) && aligned16(W);
+  dim3 grid((N + I8_BN - 1) / I8_BN, g.splits, (M + 15) / 16);
+#define PK_I8(E)                                                                          \
+  do {                                                                                    \
+    if (aligned) int8_gemm_kernel<true, E><<<grid, I8_THREADS, 0, st>>>(g);               \
+    else int8_gemm_kernel<false, E><<<grid, I8_THREADS, 0, st>>>(g);                      \
+    if (g.splits > 1) {                                                                   \
+      const int64_t total = (int64_t)M * N;                                               \
+      const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);               \
+      int8_reduce_kernel<E><<<blocks, 256, 0, st>>>(g);                                   \
+    }                                                                                     \
+  } while (0)
+  if (epi == I8_NONE) PK_I8(I8_NONE);
+  else if (epi == I8_GELU) PK_I8(I8_GELU);
+  else PK_I8(I8_RESID);
+#undef PK_I8
+  PK_LAUNCH_CHECK("int8_gemm_kernel");
+  return PK_OK;
+}
+
+}  // namespace pk
+
+using namespace pk;
+
+extern "C" {
+
+int launch_matmul_int8(const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C,
+                       int M, int N, int K, void *stream) {
+  PK_CHECK_ARG(A && Wq && scale && C, "launch_matmul_int8: null tensor pointer");
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "launch_matmul_int8: invalid shape M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return PK_OK;
+  return int8_run(I8_NONE, A, Wq, scale, C, nullptr, M, N, K, nullptr, 0, (hipStream_t)stream);
+}
+
+size_t pk_decode_mlp_int8_workspace_size(int M, int d, int F) {
+  auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
+  const size_t p = std::max(int8_workspace_bytes(M, F, d), int8_workspace_bytes(M, d, F));
+  return up((size_t)M * F * 2) + up(p);
+}
+
+int launch_decode_mlp_int8(const uint16_t *x, const int8_t *W1q, const float *s1,
+                           const int8_t *W2q, const float *s2, uint16_t *out, int M, int d, int F,
+                           void *workspace, size_t workspace_bytes, void *stream) {
+  PK_CHECK_ARG(x && W1q && s1 && W2q && s2 && out, "launch_decode_mlp_int8: null tensor pointer");
+  PK_CHECK_ARG(M >= 0 && d > 0 && F > 0, "launch_decode_mlp_int8: invalid shape");
+  if (M == 0) return PK_OK;
+  const size_t need = pk_decode_mlp_int8_workspace_size(M, d, F);
+  if (!workspace || workspace_bytes < need) {
+    set_error("launch_decode_mlp_int8: workspace of %zu bytes required, got %zu", need,
+              workspace_bytes);
+    return PK_ERR_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const size_t hbytes = ((size_t)M * F * 2 + 255) & ~size_t(255);
+  uint16_t *h = static_cast<uint16_t *>(workspace);
+  void *part = static_cast<char *>(workspace) + hbytes;
+  const size_t part_bytes = workspace_bytes - hbytes;
+  int rc = int8_run(I8_GELU, x, W1q, s1, h, nullptr, M, F, d, part, part_bytes, st);
+  if (rc) return rc;
+  return int8_run(I8_RESID, h, W2q, s2, out, x, M, d, F, part, part_bytes, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,323 @@
+"""Pin the C oracle (oracle/oracle.c) before trusting it.
+
+Checks, per function:
+  * bit-exact agreement with the reference's own kernels/cpu build (oracle/_ref,
+    compiled from /root/reference by oracle/Makefile) on seeded inputs;
+  * the hand-computed known answers of the reference's
+    tests/golden/test_golden_self.py:34-186;
+  * closed forms / invariants where the reference has no C++ (quantizer,
+    residual+rmsnorm, masked softmax, the MLP chains);
+  * the committed fixtures of tests/golden/ (reference outputs captured by
+    tests/golden/make_fixtures.py), so the pin holds where /root/reference is absent.
+"""
+from __future__ import annotations
+
+import math
+import tempfile
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from tests.helpers import bf, f32, int_bf16, rng_bf16
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- bf16 RNE
+
+def test_bf16_rne_structured_sweep(oracle):
+    """Every sign/exponent/mantissa (upper 16 bits) combined with every rounding
+    class of the dropped 16 bits, against torch's RNE conversion (an
+    independent implementation); NaNs must become quiet NaNs with the payload
+    MSB kept (kernels/cpu/cpu_reference.h:52-61)."""
+    import torch
+
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x3FFF, 0x7FFE, 0x7FFF, 0x8000, 0x8001, 0xC000, 0xFFFE, 0xFFFF],
+                    dtype=np.uint32)
+    u = (hi[:, None] | lows[None, :]).reshape(-1)
+    x = u.view(np.float32)
+    got = np.empty(x.size, dtype=np.uint16)
+    oracle.lib().pko_f32_to_bf16_array(x.ctypes.data, got.ctypes.data, x.size)
+    nan = np.isnan(x)
+    want = torch.from_numpy(x[~nan].copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got[~nan], want)
+    assert np.array_equal(got[nan], ((u[nan] >> 16) | 0x40).astype(np.uint16))
+    # ties to even, explicitly
+    assert oracle.lib().pko_f32_to_bf16(np.float32(1.0 + 2**-8)) == 0x3F80      # tie -> even (down)
+    assert oracle.lib().pko_f32_to_bf16(np.float32(1.0 + 3 * 2**-8)) == 0x3F82  # tie -> even (up)
+
+
+def test_bf16_rne_matches_reference_helper(oracle, ref):
+    r = np.random.default_rng(7)
+    u = r.integers(0, 2**32, size=20000, dtype=np.uint64).astype(np.uint32)
+    for v in u.view(np.float32)[:2000]:
+        assert oracle.lib().pko_f32_to_bf16(v) == ref.ref_f32_to_bf16(v)
+
+
+# ---------------------------------------------------------------- known answers (test_golden_self.py)
+
+def test_known_matmul_2x2(oracle):
+    out = oracle.matmul(bf([[1, 2], [3, 4]]), bf([[5, 6], [7, 8]]))
+    assert np.array_equal(f32(out), np.array([[19, 22], [43, 50]], np.float32))
+
+
+def test_known_gelu(oracle):
+    out = oracle.gelu(bf([0.0, 1.0]))
+    assert f32(out)[0] == 0.0
+    assert f32(out)[1] == np.float32(0.83984375)
+
+
+def test_known_softmax_uniform(oracle):
+    assert np.array_equal(f32(oracle.softmax(bf([[1.0, 1.0]]))), np.array([[0.5, 0.5]], np.float32))
+
+
+def test_known_rmsnorm_vector(oracle):
+    out = f32(oracle.rmsnorm(bf([[1.0, 2.0, 3.0, 4.0]])))
+    rms = math.sqrt(7.5 + 1e-5)
+    np.testing.assert_allclose(out[0], np.array([1, 2, 3, 4]) / rms, atol=4e-3, rtol=4e-3)
+
+
+def test_softmax_rows_sum_to_one(oracle):
+    x = rng_bf16((8, 16), 1, -4, 4)
+    np.testing.assert_allclose(f32(oracle.softmax(x)).sum(-1), np.ones(8), atol=2e-2)
+
+
+# ---------------------------------------------------------------- vs the reference build
+
+def test_gelu_exhaustive_vs_reference(oracle, ref):
+    x = np.arange(1 << 16, dtype=np.uint16)
+    finite = ~(((x & 0x7F80) == 0x7F80) & ((x & 0x7F) != 0))
+    ours = oracle.gelu(x)
+    theirs = np.empty_like(x)
+    ref.ref_gelu(x.ctypes.data, theirs.ctypes.data, x.size)
+    assert np.array_equal(ours[finite], theirs[finite])
+    assert np.array_equal(ours[~finite], theirs[~finite])
+
+
+@pytest.mark.parametrize("shape,with_w,eps", [((7, 130), False, 1e-5), ((64, 768), True, 1e-6),
+                                               ((33, 4096), True, 1e-6)])
+def test_rmsnorm_vs_reference(oracle, ref, shape, with_w, eps):
+    x = rng_bf16(shape, 11)
+    w = rng_bf16(shape[-1:], 12, 0.5, 1.5) if with_w else None
+    ours = oracle.rmsnorm(x, w, eps)
+    theirs = np.empty_like(x)
+    ref.ref_rmsnorm(x.ctypes.data, None if w is None else w.ctypes.data, theirs.ctypes.data,
+                    shape[0], shape[1], np.float32(eps))
+    assert np.array_equal(ours, theirs)
+
+
+@pytest.mark.parametrize("M,N,K", [(130, 65, 127), (32, 48, 256), (5, 3, 1)])
+def test_matmul_vs_reference(oracle, ref, M, N, K):
+    a, b = rng_bf16((M, K), 21), rng_bf16((K, N), 22)
+    ours = oracle.matmul(a, b)
+    theirs = np.empty((M, N), np.uint16)
+    ref.ref_matmul(a.ctypes.data, b.ctypes.data, theirs.ctypes.data, M, N, K)
+    assert np.array_equal(ours, theirs)
+
+
+def test_fused_rmsnorm_matmul_vs_reference(oracle, ref):
+    M, N, K = 24, 40, 96
+    x, w = rng_bf16((M, K), 31), rng_bf16((K, N), 32)
+    ours = oracle.fused_rmsnorm_matmul(x, w, None, 1e-6)
+    theirs = np.empty((M, N), np.uint16)
+    ref.ref_fused_rmsnorm_matmul(x.ctypes.data, w.ctypes.data, theirs.ctypes.data, M, N, K,
+                                 np.float32(1e-6))
+    assert np.array_equal(ours, theirs)
+    # with gamma == composition of the pinned primitives (golden.py:96-100)
+    g = rng_bf16((K,), 33, 0.5, 1.5)
+    assert np.array_equal(oracle.fused_rmsnorm_matmul(x, w, g, 1e-6),
+                          oracle.matmul(oracle.rmsnorm(x, g, 1e-6), w))
+
+
+def test_fused_matmul_bias_gelu_vs_reference(oracle, ref):
+    M, N, K = 17, 33, 64
+    a, b, bias = rng_bf16((M, K), 41), rng_bf16((K, N), 42), rng_bf16((N,), 43)
+    ours = oracle.fused_matmul_bias_gelu(a, b, bias)
+    theirs = np.empty((M, N), np.uint16)
+    ref.ref_fused_matmul_bias_gelu(a.ctypes.data, b.ctypes.data, bias.ctypes.data,
+                                   theirs.ctypes.data, M, N, K)
+    assert np.array_equal(ours, theirs)
+
+
+def test_softmax_vs_reference(oracle, ref):
+    x = rng_bf16((19, 1000), 51, -8, 8)
+    ours = oracle.softmax(x)
+    theirs = np.empty_like(x)
+    ref.ref_softmax(x.ctypes.data, theirs.ctypes.data, 19, 1000)
+    assert np.array_equal(ours, theirs)
+
+
+def _ref_npy_run(oracle, binary, arrays, args_after, out_name="out.npy"):
+    with tempfile.TemporaryDirectory() as d:
+        paths = []
+        for i, (kind, arr) in enumerate(arrays):
+            p = Path(d) / f"in{i}.npy"
+            if kind == "bf16":
+                oracle.save_npy_bf16(p, arr)
+            else:
+                np.save(p, arr)
+            paths.append(p)
+        outp = Path(d) / out_name
+        oracle.run_ref(binary, *args_after(paths, outp))
+        return oracle.load_npy_bf16(outp)
+
+
+@pytest.mark.parametrize("causal", [1, 0])
+@pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 2, 33, 33, 32), (1, 1, 24, 40, 40), (2, 2, 16, 48, 64)])
+def test_attention_vs_reference(oracle, B, H, Sq, Skv, D, causal):
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built")
+    q, k, v = rng_bf16((B, H, Sq, D), 61), rng_bf16((B, H, Skv, D), 62), rng_bf16((B, H, Skv, D), 63)
+    theirs = _ref_npy_run(oracle, "attention", [("bf16", q), ("bf16", k), ("bf16", v)],
+                          lambda p, o: ["prefill", p[0], p[1], p[2], o, "--causal", str(causal)])
+    ours = oracle.attention_prefill(q, k, v, None, bool(causal))
+    assert np.array_equal(ours.reshape(theirs.shape), theirs)
+
+
+def test_kv_append_vs_reference(oracle):
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built")
+    cache, new = rng_bf16((2, 3, 8, 32), 71), rng_bf16((2, 3, 5, 32), 72)
+    theirs = _ref_npy_run(oracle, "attention", [("bf16", cache), ("bf16", new)],
+                          lambda p, o: ["append", p[0], p[1], o])
+    assert np.array_equal(oracle.kv_append(cache, new), theirs.reshape(2, 3, 13, 32))
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 128), (130, 127, 65), (16, 96, 256)])
+def test_matmul_int8_vs_reference(oracle, M, N, K):
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built")
+    a = rng_bf16((M, K), 81)
+    wq, scale = oracle.quantize_per_channel(rng_bf16((K, N), 82))
+    theirs = _ref_npy_run(oracle, "matmul_quant", [("bf16", a), ("raw", wq), ("raw", scale)],
+                          lambda p, o: ["int8", p[0], p[1], p[2], o])
+    assert np.array_equal(oracle.matmul_int8(a, wq, scale), theirs.reshape(M, N))
+
+
+# ---------------------------------------------------------------- closed forms
+
+def test_quantize_closed_form(oracle):
+    w = rng_bf16((64, 40), 91, -2, 2)
+    w[:, 3] = 0  # an all-zero channel
+    wq, scale = oracle.quantize_per_channel(w)
+    wf = f32(w)
+    amax = np.abs(wf).max(0)
+    exp_scale = np.where(amax > 0, (amax / np.float32(127)).astype(np.float32), np.float32(1))
+    assert np.array_equal(scale, exp_scale.astype(np.float32))
+    assert np.all(np.abs(wq[:, np.arange(40) != 3]).max(0) == 127)
+    assert np.all(wq[:, 3] == 0) and scale[3] == 1.0
+    q = np.rint(wf / scale[None, :]).clip(-127, 127).astype(np.int8)  # numpy float32 path
+    assert np.array_equal(wq, q)
+
+
+def test_quantize_ties_round_half_even(oracle):
+    # column max 127 -> scale exactly 1.0; entries k + 0.5 must round to even.
+    col = np.array([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5], np.float32)
+    w = bf(col[:, None])
+    wq, scale = oracle.quantize_per_channel(w)
+    assert scale[0] == 1.0
+    assert list(wq[:, 0]) == [127, 0, 2, 2, 0, -2, -2, 126]
+
+
+def test_residual_rmsnorm_is_composition(oracle):
+    x, r, g = rng_bf16((9, 256), 101), rng_bf16((9, 256), 102), rng_bf16((256,), 103, 0.5, 1.5)
+    assert np.array_equal(oracle.residual_rmsnorm(x, r, g, 1e-6),
+                          oracle.rmsnorm(oracle.add(x, r), g, 1e-6))
+
+
+def test_softmax_mask_is_composition(oracle):
+    from polykernel_amd.synth import f32_to_bf16
+
+    logits = np.random.default_rng(5).normal(0, 2, size=(6, 300)).astype(np.float32)
+    mask = np.where(np.random.default_rng(6).uniform(size=(6, 300)) < 0.1, 0xFF80, 0).astype(np.uint16)
+    want = oracle.softmax(oracle.add(f32_to_bf16(logits), mask))
+    assert np.array_equal(oracle.softmax_mask(logits, mask), want)
+    assert np.all(f32(oracle.softmax_mask(logits, mask))[mask == 0xFF80] == 0.0)
+
+
+def test_attention_closed_forms(oracle):
+    # S_kv = 1 -> O = V exactly; K = 0 -> uniform weights -> O = mean of visible V.
+    q = rng_bf16((1, 2, 1, 32), 111)
+    v = rng_bf16((1, 2, 1, 32), 112)
+    k = rng_bf16((1, 2, 1, 32), 113)
+    assert np.array_equal(oracle.attention_prefill(q, k, v), v)
+    Skv = 8
+    v = int_bf16((1, 1, Skv, 16), 114, -4, 4)
+    k = np.zeros((1, 1, Skv, 16), np.uint16)
+    q = rng_bf16((1, 1, 2, 16), 115)
+    out = f32(oracle.attention_prefill(q, k, v, None, False))
+    mean = f32(v)[0, 0].mean(0)
+    np.testing.assert_allclose(out[0, 0, 0], mean, rtol=8e-3, atol=1e-6)
+
+
+def test_attention_future_invariance_and_leak_negative(oracle):
+    B, H, Sq, D = 1, 1, 8, 16
+    q, k, v = rng_bf16((B, H, Sq, D), 121), rng_bf16((B, H, Sq, D), 122), rng_bf16((B, H, Sq, D), 123)
+    base = oracle.attention_prefill(q, k, v, None, True)
+    k2, v2 = k.copy(), v.copy()
+    k2[..., -1, :] = bf(np.full(D, 3.0))
+    v2[..., -1, :] = bf(np.full(D, -7.0))
+    moved = oracle.attention_prefill(q, k2, v2, None, True)
+    assert np.array_equal(base[..., :-1, :], moved[..., :-1, :])  # only the last query sees key 7
+    leak = oracle.attention_prefill(q, k2, v2, None, False)
+    assert not np.array_equal(base[..., :-1, :], leak[..., :-1, :])
+
+
+def test_mlp_block_is_composition(oracle):
+    M, d, F = 4, 64, 128
+    x, g = rng_bf16((M, d), 131), rng_bf16((d,), 132, 0.5, 1.5)
+    w1, b1 = rng_bf16((d, F), 133, -0.2, 0.2), rng_bf16((F,), 134, -0.05, 0.05)
+    w2, b2 = rng_bf16((F, d), 135, -0.1, 0.1), rng_bf16((d,), 136, -0.05, 0.05)
+    a = oracle.rmsnorm(x, g, 1e-6)
+    h = oracle.fused_matmul_bias_gelu(a, w1, b1)
+    y = oracle.fused_matmul_bias_residual(h, w2, b2, x)
+    assert np.array_equal(oracle.mlp_block(x, g, w1, b1, w2, b2, 1e-6), y)
+    # the residual chain is add(bias(matmul)) stage by stage
+    t = oracle.matmul(h, w2)
+    from polykernel_amd.synth import bf16_to_f32, f32_to_bf16
+    u = f32_to_bf16(bf16_to_f32(t) + bf16_to_f32(b2)[None, :])
+    assert np.array_equal(y, oracle.add(u, x))
+
+
+def test_decode_chain_is_composition(oracle):
+    M, d, F = 3, 64, 96
+    x = rng_bf16((M, d), 141)
+    w1q, s1 = oracle.quantize_per_channel(rng_bf16((d, F), 142))
+    w2q, s2 = oracle.quantize_per_channel(rng_bf16((F, d), 143))
+    h = oracle.gelu(oracle.matmul_int8(x, w1q, s1))
+    want = oracle.add(oracle.matmul_int8(h, w2q, s2), x)
+    assert np.array_equal(oracle.decode_mlp_int8(x, w1q, s1, w2q, s2), want)
+
+
+def test_thread_count_does_not_change_bits(oracle):
+    a, b = rng_bf16((37, 200), 151), rng_bf16((200, 61), 152)
+    n = oracle.num_threads()
+    oracle.set_num_threads(1)
+    one = oracle.matmul(a, b)
+    oracle.set_num_threads(max(n, 2))
+    many = oracle.matmul(a, b)
+    oracle.set_num_threads(n)
+    assert np.array_equal(one, many)
+
+
+# ---------------------------------------------------------------- committed fixtures
+
+def _fixtures():
+    p = GOLDEN / "ref_vectors.npz"
+    if not p.exists():
+        pytest.skip("tests/golden/ref_vectors.npz not generated")
+    return np.load(p, allow_pickle=False)
+
+
+def test_oracle_matches_committed_reference_vectors(oracle):
+    z = _fixtures()
+    assert np.array_equal(oracle.rmsnorm(z["rms_x"], z["rms_w"], float(z["rms_eps"])), z["rms_out"])
+    assert np.array_equal(oracle.matmul(z["mm_a"], z["mm_b"]), z["mm_out"])
+    assert np.array_equal(oracle.fused_matmul_bias_gelu(z["mbg_a"], z["mbg_b"], z["mbg_bias"]), z["mbg_out"])
+    assert np.array_equal(oracle.gelu(np.arange(1 << 16, dtype=np.uint16)), z["gelu_table"])
+    assert np.array_equal(oracle.softmax(z["sm_x"]), z["sm_out"])
+    assert np.array_equal(oracle.attention_prefill(z["att_q"], z["att_k"], z["att_v"], None, True),
+                          z["att_out"])
+    assert np.array_equal(oracle.matmul_int8(z["i8_a"], z["i8_wq"], z["i8_scale"]), z["i8_out"])
