@@ -1,0 +1,351 @@
+#!/usr/bin/env python3
+"""Benchmark: the config-2 fused MLP block on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+
+A step is one pass of the MLP block over the config-2 batch (BASELINE.json
+configs[1]): RMSNorm(x, gamma) -> MatMul W1 [4096,16384] + b1 -> GELU(erf) ->
+MatMul W2 [16384,4096] + b2 -> + x, x bf16 [4096,4096], synthetic seeded inputs
+resident in HBM before timing.  The step issues the same three C-ABI launches
+launch_mlp_block makes (rmsnorm, GEMM+bias+GELU, GEMM+bias+residual), with HIP
+events around the dominant GEMM launch on the stream it runs on.
+
+value = 2^40 algorithmic FLOP per step / wall time per step (TFLOP/s).
+The other BASELINE configs (attention prefill, residual+RMSNorm, masked
+softmax, int8 decode, RMSNorm->MatMul) are reported under "extra", and the
+CPU oracle is timed on a bounded row sample under "cpu_baseline".
+One JSON line is printed.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "fused-MLP TFLOP/s (% bf16 MFMA peak); attn-prefill TFLOP/s; GB/s; 1×MI355X"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+SEED = 0xC0FFEE
+
+M, D, F = 4096, 4096, 16384
+MLP_FLOP = 2 * M * D * F * 2           # 2^40
+GEMM_FLOP = 2 * M * D * F              # per GEMM launch
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def dev_bf16(a):
+    import numpy as np
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def event_pair():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def bench_mlp(steps: int, warmup: int):
+    import numpy as np
+    import torch
+
+    from polykernel_amd import _lib, synth
+    from polykernel_amd._lib import check
+
+    lib = _lib.load()
+    t0 = time.time()
+    x = synth.normal_bf16((M, D), 1, seed=SEED)
+    g = synth.normal_bf16((D,), 2, 0.1, 1.0, seed=SEED)
+    w1 = synth.normal_bf16((D, F), 3, 1.0 / math.sqrt(D), seed=SEED)
+    b1 = synth.normal_bf16((F,), 4, 0.02, seed=SEED)
+    w2 = synth.normal_bf16((F, D), 5, 1.0 / math.sqrt(F), seed=SEED)
+    b2 = synth.normal_bf16((D,), 6, 0.02, seed=SEED)
+    tx, tg, tw1, tb1, tw2, tb2 = map(dev_bf16, (x, g, w1, b1, w2, b2))
+    a = torch.empty(M, D, dtype=torch.bfloat16, device="cuda")
+    h = torch.empty(M, F, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(M, D, dtype=torch.bfloat16, device="cuda")
+    log(f"mlp inputs ready in {time.time() - t0:.1f}s")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(ev=None):
+        check(lib.launch_rmsnorm(tx.data_ptr(), tg.data_ptr(), a.data_ptr(), M, D, 1e-6, sp), "rmsnorm")
+        if ev is not None:
+            ev[0].record(stream)
+        check(lib.pk_gemm_ex(1, a.data_ptr(), tw1.data_ptr(), h.data_ptr(), tb1.data_ptr(), None,
+                             M, F, D, -1, sp), "gemm1")
+        if ev is not None:
+            ev[1].record(stream)
+            ev[2].record(stream)
+        check(lib.pk_gemm_ex(2, h.data_ptr(), tw2.data_ptr(), y.data_ptr(), tb2.data_ptr(), tx.data_ptr(),
+                             M, D, F, -1, sp), "gemm2")
+        if ev is not None:
+            ev[3].record(stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    g1 = [e[0].elapsed_time(e[1]) for e in evs]
+    g2 = [e[2].elapsed_time(e[3]) for e in evs]
+
+    # the product entry point on the same buffers (equal work; reported for reference)
+    ws = torch.empty(lib.pk_mlp_block_workspace_size(M, D, F), dtype=torch.uint8, device="cuda")
+    e0, e1 = event_pair()
+    e0.record(stream)
+    for _ in range(3):
+        check(lib.launch_mlp_block(tx.data_ptr(), tg.data_ptr(), tw1.data_ptr(), tb1.data_ptr(),
+                                   tw2.data_ptr(), tb2.data_ptr(), y.data_ptr(), M, D, F, 1e-6,
+                                   ws.data_ptr(), ws.numel(), sp), "launch_mlp_block")
+    e1.record(stream)
+    torch.cuda.synchronize()
+    entry_ms = e0.elapsed_time(e1) / 3
+    inputs = dict(x=x, g=g, w1=w1, b1=b1, w2=w2, b2=b2)
+    return elapsed, g1, g2, entry_ms, inputs
+
+
+def bench_extra(reps: int = 20):
+    """Other BASELINE configs: one timing each (HIP events, warm)."""
+    import numpy as np
+    import torch
+
+    from polykernel_amd import _lib, kernels, synth
+    from polykernel_amd._lib import check
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    out = {}
+
+    def timeit(fn, n=reps, warm=3):
+        for _ in range(warm):
+            fn()
+        e0, e1 = event_pair()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    # config 1: RMSNorm -> MatMul fragment (cache-resident)
+    x = dev_bf16(synth.normal_bf16((128, 768), 11))
+    g = dev_bf16(synth.normal_bf16((768,), 12, 0.1, 1.0))
+    w = dev_bf16(synth.normal_bf16((768, 3072), 13, 1 / math.sqrt(768)))
+    o = torch.empty(128, 3072, dtype=torch.bfloat16, device="cuda")
+    ms = timeit(lambda: check(lib.launch_fused_rmsnorm_matmul_gamma(
+        x.data_ptr(), g.data_ptr(), w.data_ptr(), o.data_ptr(), 128, 3072, 768, 1e-6, sp), "cfg1"))
+    out["rmsnorm_matmul_cfg1"] = {"us": round(ms * 1e3, 2),
+                                  "tflops": round(2 * 128 * 3072 * 768 / (ms * 1e-3) / 1e12, 2),
+                                  "note": "warm, L2/MALL-resident (5.7 MB)"}
+    del x, g, w, o
+
+    # config 3: KV append (in place) + causal prefill, B1 H32 D128, 3584 + 512
+    B, H, Sc, Sn, Dh = 1, 32, 3584, 512, 128
+    q = dev_bf16(synth.normal_bf16((B, H, Sn, Dh), 21))
+    kn = dev_bf16(synth.normal_bf16((B, H, Sn, Dh), 22))
+    vn = dev_bf16(synth.normal_bf16((B, H, Sn, Dh), 23))
+    kc = torch.empty(B, H, Sc + Sn, Dh, dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    kc[:, :, :Sc] = dev_bf16(synth.normal_bf16((B, H, Sc, Dh), 24))
+    vc[:, :, :Sc] = dev_bf16(synth.normal_bf16((B, H, Sc, Dh), 25))
+    o = torch.empty_like(q)
+    ms = timeit(lambda: check(lib.launch_fused_kv_append_attention(
+        q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kn.data_ptr(), vn.data_ptr(), o.data_ptr(),
+        B, H, Sn, Sc, Dh, Sc + Sn, 1 / math.sqrt(Dh), 1, sp), "cfg3"))
+    flop = 32216449024
+    tf = flop / (ms * 1e-3) / 1e12
+    out["attention_prefill_cfg3"] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 2),
+                                     "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4)}
+    del q, kn, vn, kc, vc, o
+
+    # config 4a: residual + RMSNorm [16384, 8192]
+    R, C = 16384, 8192
+    xa = dev_bf16(synth.normal_bf16((R, C), 31))
+    ra = dev_bf16(synth.normal_bf16((R, C), 32))
+    ga = dev_bf16(synth.normal_bf16((C,), 33, 0.1, 1.0))
+    oa = torch.empty_like(xa)
+    ms = timeit(lambda: check(lib.launch_fused_residual_rmsnorm(
+        xa.data_ptr(), ra.data_ptr(), ga.data_ptr(), oa.data_ptr(), R, C, 1e-6, sp), "cfg4a"))
+    gbs = 805322752 / (ms * 1e-3) / 1e9
+    out["residual_rmsnorm_cfg4a"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    del xa, ra, ga, oa
+
+    # config 4b: masked softmax fp32 logits [16384, 8192] + bf16 additive mask
+    lg = torch.from_numpy(synth.normal_f32((R, C), 34, 2.0)).cuda()
+    mk = dev_bf16(synth.mask_bf16((R, C), 35, 0.1))
+    om = torch.empty(R, C, dtype=torch.bfloat16, device="cuda")
+    ms = timeit(lambda: check(lib.launch_fused_softmax_mask(lg.data_ptr(), mk.data_ptr(), om.data_ptr(),
+                                                            R, C, sp), "cfg4b"))
+    gbs = 1073741824 / (ms * 1e-3) / 1e9
+    out["masked_softmax_cfg4b"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    del lg, mk, om
+
+    # config 5: int8 decode MLP, M=16, 8192 <-> 28672 (weights quantised on the GPU)
+    Md, dd, Fd = 16, 8192, 28672
+    xd = dev_bf16(synth.normal_bf16((Md, dd), 41))
+    w1q, s1 = kernels.quantize_per_channel(dev_bf16(synth.normal_bf16((dd, Fd), 42, 1 / math.sqrt(dd))))
+    w2q, s2 = kernels.quantize_per_channel(dev_bf16(synth.normal_bf16((Fd, dd), 43, 1 / math.sqrt(Fd))))
+    torch.cuda.empty_cache()
+    ws = torch.empty(lib.pk_decode_mlp_int8_workspace_size(Md, dd, Fd), dtype=torch.uint8, device="cuda")
+    od = torch.empty_like(xd)
+    ms = timeit(lambda: check(lib.launch_decode_mlp_int8(
+        xd.data_ptr(), w1q.data_ptr(), s1.data_ptr(), w2q.data_ptr(), s2.data_ptr(), od.data_ptr(),
+        Md, dd, Fd, ws.data_ptr(), ws.numel(), sp), "cfg5"))
+    gbs = 470433792 / (ms * 1e-3) / 1e9
+    out["int8_decode_mlp_cfg5"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    return out
+
+
+def cpu_baseline(inputs, budget_s: float = 12.0):
+    """Oracle (C port of kernels/cpu) on a row sample of the same workload."""
+    import numpy as np
+
+    from oracle import pyoracle
+
+    lib = pyoracle.lib()
+    threads = pyoracle.num_threads()
+    x = inputs["x"]
+    rows = 16
+    t0 = time.perf_counter()
+    pyoracle.mlp_block(x[:rows], inputs["g"], inputs["w1"], inputs["b1"], inputs["w2"], inputs["b2"], 1e-6)
+    dt = time.perf_counter() - t0
+    more = int(max(0, min(M - rows, rows * (budget_s / max(dt, 1e-3) - 1))))
+    more = (more // 16) * 16
+    if more > 0:
+        t1 = time.perf_counter()
+        pyoracle.mlp_block(x[rows:rows + more], inputs["g"], inputs["w1"], inputs["b1"], inputs["w2"],
+                           inputs["b2"], 1e-6)
+        dt += time.perf_counter() - t1
+        rows += more
+    flop = rows * 2 * (D * F + F * D)
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of {M} rows of the config-2 MLP block (rows are independent) in "
+                      f"{dt:.1f}s; oracle/oracle.c -O2 -ffp-contract=off, OpenMP over rows"}
+
+
+def read_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary, if any."""
+    p = ROOT / "profiles" / "gemm_bias_gelu_mlp_config2_pmc.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch="):
+            try:
+                return int(float(line.split("=", 1)[1]))
+            except ValueError:
+                return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only time a 1 GiB device-to-device copy (HBM ceiling and the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(the kernels run on one MI355X; see DESIGN.md for how the path would shard)",
+              file=sys.stderr, flush=True)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    if args.calibrate_copy:
+        n = 1 << 30
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        e0, e1 = event_pair()
+        e0.record()
+        for _ in range(10):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 10
+        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "ms": round(ms, 4),
+                          "gbs_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
+    from polykernel_amd import _lib
+
+    _lib.load()
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    elapsed, g1, g2, entry_ms, inputs = bench_mlp(args.steps, args.warmup)
+    ms_step = elapsed / args.steps * 1e3
+    value = MLP_FLOP / (ms_step * 1e-3) / 1e12
+    g1_ms = sum(g1) / len(g1)
+    g2_ms = sum(g2) / len(g2)
+    achieved = GEMM_FLOP / (g1_ms * 1e-3) / 1e12
+    log(f"mlp step {ms_step:.3f} ms -> {value:.1f} TFLOP/s; gemm1 {g1_ms:.3f} ms, gemm2 {g2_ms:.3f} ms")
+    extra = {}
+    if not args.no_extra:
+        extra = bench_extra()
+        log(f"extra: {json.dumps(extra)}")
+    extra["mlp_block_breakdown"] = {
+        "gemm1_bias_gelu_ms": round(g1_ms, 4), "gemm2_bias_residual_ms": round(g2_ms, 4),
+        "gemm2_tflops": round(GEMM_FLOP / (g2_ms * 1e-3) / 1e12, 1),
+        "launch_mlp_block_ms": round(entry_ms, 4),
+        "frac_mfma_block": round(value / PEAK_BF16_TFLOPS, 4)}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(inputs)
+        log(f"cpu baseline: {cpu}")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/N(0,1/fan_in) bf16, BASELINE config 2)",
+        "config": {"workload": "MLP block config2: RMSNorm(x)->x@W1[4096,16384]+b1->GELU(erf)->"
+                               "@W2[16384,4096]+b2->+x, x bf16 [4096,4096]",
+                   "tokens": M, "d": D, "ffn": F, "flop_per_step": MLP_FLOP},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": read_traffic(),
+                     "kernel": "gemm_kernel<256,256,2,4,EPI_BIAS_GELU> (GEMM1, 2^39 FLOP/launch)"},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -56,6 +56,11 @@ PK_API int pk_device_arch(int ordinal, char *buf, int buf_len);
  * Mirrors ParseGcnArchName, lib/Runtime/DeviceDetect.cpp:28-50. */
 PK_API int pk_parse_gcn_arch_name(const char *gcn_arch_name, char *buf, int buf_len);
 
+/* Device self-check: counts the fp32 inputs (all 2^32) on which the kernels'
+ * fp32 -> bf16 conversion differs from the reference RNE formula
+ * (kernels/cpu/cpu_reference.h:52-61).  Synchronous; allocates 8 bytes. */
+PK_API int pk_check_bf16_conversion(unsigned long long *mismatches);
+
 /* ---- reference entry points (same names and argument order) ------------ */
 
 /* y = bf16(x / sqrt(mean(x^2) + eps) [* w]); w may be NULL.
@@ -160,11 +165,16 @@ PK_API int launch_decode_mlp_int8(const uint16_t *x, const int8_t *W1q, const fl
                            void *workspace, size_t workspace_bytes, void *stream);
 
 /* Tuning/test hook: one GEMM with an explicit epilogue (0 none, 1 bias+GELU,
- * 2 bias+residual, 3 residual) and tile (0: 256x256, 1: 128x128, 2: 64x64,
- * -1: heuristic).  Same numerics as the entry points above. */
+ * 2 bias+residual, 3 residual) and tile (0: 256x256, DMA-pipelined when
+ * K % 32 == 0; 1: 128x128; 2: 64x64; 3: register-staged 256x256; -1: heuristic).
+ * Same numerics as the entry points above. */
 PK_API int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C,
                       const uint16_t *bias, const uint16_t *R, int M, int N, int K, int tile,
                       void *stream);
+
+/* Tuning hook: k-tiles in flight in the DMA-pipelined GEMM's LDS ring (4 or 5;
+ * 5 uses all 160 KiB of LDS).  Process-wide; default 5. */
+PK_API int pk_gemm_set_ring_depth(int depth);
 
 /* ---- synthetic inputs (host, deterministic, OpenMP) -------------------- */
 

@@ -45,6 +45,7 @@ SIGNATURES = {
     "pk_init": (I, []),
     "pk_device_arch": (I, [I, C.c_char_p, I]),
     "pk_parse_gcn_arch_name": (I, [C.c_char_p, C.c_char_p, I]),
+    "pk_check_bf16_conversion": (I, [C.POINTER(C.c_ulonglong)]),
     "launch_rmsnorm": (I, [P, P, P, I, I, F, P]),
     "launch_gelu": (I, [P, P, I, P]),
     "launch_matmul": (I, [P, P, P, I, I, I, P]),
@@ -65,6 +66,7 @@ SIGNATURES = {
     "pk_decode_mlp_int8_workspace_size": (SZ, [I, I, I]),
     "launch_decode_mlp_int8": (I, [P, P, P, P, P, P, I, I, I, P, SZ, P]),
     "pk_gemm_ex": (I, [I, P, P, P, P, P, I, I, I, I, P]),
+    "pk_gemm_set_ring_depth": (I, [I]),
     "pk_synth_normal_bf16": (None, [U64, U64, D, D, P, I64]),
     "pk_synth_normal_f32": (None, [U64, U64, D, D, P, I64]),
     "pk_synth_mask_bf16": (None, [U64, U64, D, P, I64]),

@@ -32,6 +32,9 @@ COMMON_FLAGS = [
     "-fPIC",
     "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # fully unroll the GEMM epilogues (256 accumulators per lane): above the
+    # default threshold the accumulator array is demoted to scratch memory
+    "-mllvm", "-pragma-unroll-threshold=1000000",
     "-Wno-unused-result",
     "-I", str(PKG.parent / "include"),
 ]

@@ -37,30 +37,32 @@ int hip_fail(hipError_t e, const char *what) {
   return e == hipErrorNoDevice ? PK_ERR_NO_DEVICE : PK_ERR_HIP;
 }
 
-// GELU over every bf16 code, following kernels/cpu/cpu_reference.cpp:46-55:
+// The compact GELU table (pk_common.hpp, gelu_bits): entry i is the bf16 GELU
+// of gelu_table_code(i), evaluated as kernels/cpu/cpu_reference.cpp:46-55 does:
 // e = (float)erf((double)(x * 0.70710678f)); y = bf16((0.5f * x) * (1.0f + e)).
-// NaN codes map to their quiet form and -inf to the x86 default NaN (0xFFC0),
-// which is what that host arithmetic produces for those inputs.
-__device__ uint16_t g_gelu_table_storage[65536];
+__device__ uint16_t g_gelu_table_storage[GELU_TABLE_SIZE];
 
 __global__ void gelu_table_init_kernel(uint16_t *tab) {
 #pragma clang fp contract(off)
-  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= 65536u) return;
-  const uint32_t exp_bits = b & 0x7F80u, man = b & 0x007Fu;
-  if (exp_bits == 0x7F80u && man != 0u) {
-    tab[b] = (uint16_t)(b | 0x0040u);
-    return;
-  }
-  if (b == 0xFF80u) {
-    tab[b] = 0xFFC0u;
-    return;
-  }
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= GELU_TABLE_SIZE) return;
   const float kInvSqrt2 = 0.70710678118654752440f;
-  const float x = bf2f(b);
+  const float x = bf2f(gelu_table_code(i));
   const float e = (float)erf((double)(x * kInvSqrt2));
   const float y = (0.5f * x) * (1.0f + e);
-  tab[b] = (uint16_t)f2bf(y);
+  tab[i] = (uint16_t)f2bf(y);
+}
+
+// Exhaustive device self-check: f2bf (hardware conversion) against the
+// reference formula over all 2^32 fp32 bit patterns.
+__global__ void bf16_selfcheck_kernel(unsigned long long *bad) {
+  const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long n = 0;
+  for (uint32_t j = 0; j < 1024; ++j) {
+    const uint32_t u = (uint32_t)(tid * 1024u + j);
+    n += f2bf(__uint_as_float(u)) != f2bf_formula(__uint_as_float(u));
+  }
+  if (n) atomicAdd(bad, n);
 }
 
 int gelu_table(const uint16_t **table) {
@@ -75,7 +77,7 @@ int gelu_table(const uint16_t **table) {
     void *p = nullptr;
     PK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_gelu_table_storage)));
     uint16_t *tab = static_cast<uint16_t *>(p);
-    gelu_table_init_kernel<<<256, 256, 0, nullptr>>>(tab);
+    gelu_table_init_kernel<<<(GELU_TABLE_SIZE + 255) / 256, 256, 0, nullptr>>>(tab);
     PK_LAUNCH_CHECK("gelu_table_init_kernel");
     // One-time set-up: make the table visible to every stream before use.
     PK_HIP(hipDeviceSynchronize());
@@ -174,6 +176,24 @@ const char *pk_last_error(void) { return g_err; }
 int pk_init(void) {
   const uint16_t *t = nullptr;
   return gelu_table(&t);
+}
+
+int pk_check_bf16_conversion(unsigned long long *mismatches) {
+  if (!mismatches) {
+    set_error("pk_check_bf16_conversion: null argument");
+    return PK_ERR_INVALID_ARG;
+  }
+  unsigned long long *d = nullptr;
+  PK_HIP(hipMalloc(&d, sizeof(unsigned long long)));
+  hipError_t e = hipMemset(d, 0, sizeof(unsigned long long));
+  if (e == hipSuccess) {
+    bf16_selfcheck_kernel<<<(1u << 22) / 256, 256>>>(d);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(mismatches, d, sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "pk_check_bf16_conversion");
+  return PK_OK;
 }
 
 int pk_parse_gcn_arch_name(const char *name, char *buf, int buf_len) {

@@ -17,9 +17,11 @@
 // Epilogues reproduce the golden per-stage bf16 rounding
 // (tests/golden/golden.py:48-66, kernels/cpu/cpu_reference.cpp:92-105):
 //   EPI_NONE        c = bf16(acc)
-//   EPI_BIAS_GELU   c = gelu(bf16(bf16(acc) + bias[n]))      (GELU by exact table)
+//   EPI_BIAS_GELU   c = gelu(bf16(bf16(acc) + bias[n]))      (exact GELU, gelu_bits)
 //   EPI_BIAS_RESID  c = bf16(bf16(bf16(acc) + bias[n]) + R[m,n])
 //   EPI_RESID       c = bf16(bf16(acc) + R[m,n])
+#include <type_traits>
+
 #include "pk_common.hpp"
 
 namespace pk {
@@ -75,12 +77,33 @@ __device__ __forceinline__ uint16_t epilogue(float acc, int m, int n, const Gemm
     return (uint16_t)f2bf(acc);
   } else if constexpr (EPI == EPI_BIAS_GELU) {
     const uint32_t u = f2bf(t + bias_n);
-    return g.gelu_tab[u];
+    return (uint16_t)gelu_bits(u, g.gelu_tab);
   } else if constexpr (EPI == EPI_BIAS_RESID) {
     const float u = bf2f(f2bf(t + bias_n));
     return (uint16_t)f2bf(u + bf2f(g.R[(size_t)m * g.N + n]));
   } else {
     return (uint16_t)f2bf(t + bf2f(g.R[(size_t)m * g.N + n]));
+  }
+}
+
+// One 32x32 accumulator block of this lane: element i is row mb + (i/4)*8 + i%4
+// of column n.  All epilogue loads (GELU table, residual) are issued before
+// any store so they overlap instead of serialising load -> store pairs.
+template <int EPI>
+__device__ __forceinline__ void store_block(const f32x16 &acc, int mb, int n, bool nok,
+                                            const GemmArgs &g, float bias_n) {
+  uint16_t v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = mb + (i >> 2) * 8 + (i & 3);
+    const int mc = min(m, g.M - 1);
+    v[i] = epilogue<EPI>(acc[i], mc, nok ? n : 0, g, bias_n);
+  }
+  if (!nok) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = mb + (i >> 2) * 8 + (i & 3);
+    if (m < g.M) g.C[(size_t)m * g.N + n] = v[i];
   }
 }
 
@@ -251,12 +274,329 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
       bias_n = (nok && g.bias) ? bf2f(g.bias[n]) : 0.f;
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
+      const int mb = m0 + wm * TM + fm * 32 + (lane >> 5) * 4;
+      store_block<EPI>(acc[fm][fn], mb, n, nok, g, bias_n);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Large-tile GEMM (the MLP block path).  256x256 per workgroup, 4 waves in a
+// 2x2 grid, each wave owning a 128x128 sub-tile (16 MFMA accumulator blocks,
+// 256 fp32 per lane, held in AGPRs).  K advances in tiles of 32 through a
+// 4-stage LDS ring filled by global_load_lds_dwordx4 (global -> LDS without
+// VGPR staging) issued three tiles ahead.  Per k-tile and wave:
+//     read B/A fragments of substep 1 | MFMAs of substep 0 |
+//     wait own DMA of tile t+1, s_barrier, DMA tile t+4 into the freed stage |
+//     read fragments of tile t+1 substep 0 | MFMAs of substep 1
+// so the single barrier sits behind queued MFMA work and every LDS read is
+// issued one substep before its use.  Requires K % 32 == 0, N % 8 == 0 and
+// 16-byte aligned A/B; out-of-range rows/columns are clamped to valid memory
+// (their results are never stored).
+// ---------------------------------------------------------------------------
+constexpr int G2_BM = 256, G2_BN = 256, G2_BK = 32, G2_STAGES = 4;
+constexpr int G2_THREADS = 256;
+constexpr int G2_DMA_PER_TILE = 8;  // 1 KiB global_load_lds per wave per tile: 4 for A, 4 for B
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ int swz_a32(int row) { return (row >> 1) & 3; }
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt in bits [3:0] and [15:14],
+// expcnt [6:4], lgkmcnt [11:8]; expcnt and lgkmcnt left at "no wait".
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+
+__device__ __forceinline__ void vm_wait(int n_tiles) {
+  // wait until at most n_tiles * G2_DMA_PER_TILE of this wave's DMA loads are in flight
+  if (n_tiles >= 3) __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * G2_DMA_PER_TILE));
+  else if (n_tiles == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * G2_DMA_PER_TILE));
+  else if (n_tiles == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(G2_DMA_PER_TILE));
+  else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+}
+
+template <int EPI, int STAGES>
+__global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
+  static_assert(STAGES == 4 || STAGES == 5, "ring depth");
+  constexpr int A_STAGE = G2_BM * G2_BK;  // elements
+  constexpr int B_STAGE = G2_BK * G2_BN;
+  // One array per ring stage: distinct LDS objects let the compiler see that a
+  // DMA into one stage does not alias reads of another, so it adds no waits of
+  // its own; the explicit vmcnt waits below order each stage.
+  __shared__ __attribute__((aligned(1024))) uint16_t As0[A_STAGE], As1[A_STAGE], As2[A_STAGE], As3[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t Bs0[B_STAGE], Bs1[B_STAGE], Bs2[B_STAGE], Bs3[B_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t As4[STAGES > 4 ? A_STAGE : 8], Bs4[STAGES > 4 ? B_STAGE : 8];
+  auto a_stage = [&](auto c) -> uint16_t * {
+    constexpr int st = decltype(c)::value;
+    if constexpr (st == 0) return As0;
+    else if constexpr (st == 1) return As1;
+    else if constexpr (st == 2) return As2;
+    else if constexpr (st == 3) return As3;
+    else return As4;
+  };
+  auto b_stage = [&](auto c) -> uint16_t * {
+    constexpr int st = decltype(c)::value;
+    if constexpr (st == 0) return Bs0;
+    else if constexpr (st == 1) return Bs1;
+    else if constexpr (st == 2) return Bs2;
+    else if constexpr (st == 3) return Bs3;
+    else return Bs4;
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave index as a scalar: every LDS destination (M0) below is then computed
+  // in scalar registers
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid >> 1, wn = wid & 1;
+  const int tm = (g.M + G2_BM - 1) / G2_BM, tn = (g.N + G2_BN - 1) / G2_BN;
+  int mt, nt;
+  tile_coords(blockIdx.x, tm, tn, mt, nt);
+  const int m0 = mt * G2_BM, n0 = nt * G2_BN;
+  const int KT = g.K / G2_BK;
+
+  // ---- DMA sources: buffer_load ... lds with a resource descriptor per
+  // operand (A: rows m0.., B: columns n0..), a loop-invariant per-lane byte
+  // offset (voffset) and the per-tile advance as the scalar soffset, so the
+  // issue needs no address arithmetic in vector registers.
+  // A: wave w, instr j covers rows 64w + 16j + lane/4, physical chunk lane%4.
+  uint32_t a_off[4];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = m0 + wm * TM + fm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-        if (nok && m < g.M) g.C[(size_t)m * g.N + n] = epilogue<EPI>(acc[fm][fn][i], m, n, g, bias_n);
+  for (int j = 0; j < 4; ++j) {
+    const int r = 64 * wid + 16 * j + (lane >> 2);
+    const int c = (lane & 3) ^ swz_a32(r);
+    const int rr = min(r, g.M - 1 - m0);
+    a_off[j] = (uint32_t)(rr * g.K + 8 * c) * 2u;
+  }
+  // B: wave w, instr j covers rows 8w + 2j + lane/32, physical chunk lane%32.
+  uint32_t b_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 8 * wid + 2 * j + (lane >> 5);
+    const int c = (lane & 31) ^ swz_b<G2_BN>(r);
+    const int cc = min(8 * c, g.N - 8 - n0);
+    b_off[j] = (uint32_t)(r * g.N + cc) * 2u;
+  }
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(g.A + (size_t)m0 * g.K), (short)0, (g.M - m0) * g.K * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(g.B + n0), (short)0, (g.K * g.N - n0) * 2, 0x00020000);
+  auto issue_one = [&](auto c, int t, int j) {
+    if (j < 4)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)&a_stage(c)[(64 * wid + 16 * j) * G2_BK],
+                                               16, a_off[j], t * (G2_BK * 2), 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc,
+                                               (lds_void *)&b_stage(c)[(8 * wid + 2 * (j - 4)) * G2_BN], 16,
+                                               b_off[j - 4], t * (G2_BK * 2) * g.N, 0, 0);
+  };
+  auto issue = [&](auto c, int t) {
+#pragma unroll
+    for (int j = 0; j < G2_DMA_PER_TILE; ++j) issue_one(c, t, j);
+  };
+
+  // ---- per-lane fragment read offsets (elements within a stage)
+  int a_rd[4][2];
+#pragma unroll
+  for (int fm = 0; fm < 4; ++fm) {
+    const int row = wm * 128 + fm * 32 + (lane & 31);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int c = 2 * s + (lane >> 5);
+      a_rd[fm][s] = row * G2_BK + ((c ^ swz_a32(row)) << 3);
+    }
+  }
+  const int grp = lane >> 4, gi = lane & 15;
+  int b_rd[4][2][2];
+#pragma unroll
+  for (int fn = 0; fn < 4; ++fn)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int k = 16 * s + 8 * (grp >> 1) + 4 * r + (gi >> 2);
+        const int col = wn * 128 + fn * 32 + 16 * (grp & 1) + 4 * (gi & 3);
+        const int c = col >> 3;
+        b_rd[fn][s][r] = k * G2_BN + ((c ^ swz_b<G2_BN>(k)) << 3) + (col & 7);
+      }
+
+  struct Frag {
+    bf16x8 a[4];
+    bf16x8 b[4];
+  };
+  // Fragment reads in 8 units (u < 4: A block u; u >= 4: B block u-4, two
+  // transpose reads joined without repacking) so they can be spread over the
+  // MFMA stream.  (Measured: this order beats issuing them in order of first
+  // use.)
+  auto read_unit = [&](Frag &f, auto c, int s, int u) {
+    const uint16_t *as = a_stage(c);
+    const uint16_t *bs = b_stage(c);
+    const int fm = u;
+    if (u < 4) {
+      f.a[fm] = lds_read_a(as + a_rd[fm][s]);
+    } else {
+      const int fn = u - 4;
+      const i16x4 h0 = lds_read_tr(bs + b_rd[fn][s][0]);
+      const i16x4 h1 = lds_read_tr(bs + b_rd[fn][s][1]);
+      f.b[fn] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+  auto read_frag = [&](Frag &f, auto c, int s) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) read_unit(f, c, s, u);
+  };
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  auto mfma_one = [&](const Frag &f, int i) {
+    acc[i >> 2][i & 3] =
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i >> 2], f.b[i & 3], acc[i >> 2][i & 3], 0, 0, 0);
+  };
+
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  using S4 = std::integral_constant<int, 4>;
+
+  // ---- prologue: tiles 0..STAGES-1 in flight (indices past the end are
+  // clamped to the last tile: every k-tile issues the same number of DMA
+  // loads, so each wait below is a compile-time vmcnt), wait for tile 0.
+  issue(S0{}, 0);
+  issue(S1{}, min(1, KT - 1));
+  issue(S2{}, min(2, KT - 1));
+  issue(S3{}, min(3, KT - 1));
+  if constexpr (STAGES > 4) issue(S4{}, min(4, KT - 1));
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * G2_DMA_PER_TILE));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  Frag f0, f1;
+  read_frag(f0, S0{}, 0);
+  // One k-tile on ring stage C (tile t, t % STAGES == C):
+  //   16 MFMAs on substep 0, a fragment-read unit of substep 1 after every
+  //   second MFMA;
+  //   wait for this wave's reads of the stage and its DMA of tile t+1, barrier;
+  //   16 MFMAs on substep 1, alternating a DMA load of tile t+STAGES (into the
+  //   stage just released) and a read unit of tile t+1's substep 0.
+  auto body = [&](auto c, int t) {
+    constexpr int st = decltype(c)::value;
+    using Next = std::integral_constant<int, (st + 1) % STAGES>;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mfma_one(f0, i);
+      if ((i & 1) == 0) read_unit(f1, c, 1, i >> 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // this wave's reads of stage st are done and its DMA of tile t+1 landed
+    // (STAGES-2 newer tiles may still be in flight); then all waves agree.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * G2_DMA_PER_TILE));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const int tn_dma = min(t + STAGES, KT - 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mfma_one(f1, i);
+      if ((i & 1) == 1) issue_one(c, tn_dma, i >> 1);
+      if ((i & 1) == 0) read_unit(f0, Next{}, 0, i >> 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int t = 0; t < KT; t += STAGES) {
+    body(S0{}, t);
+    if (t + 1 < KT) body(S1{}, t + 1);
+    if (t + 2 < KT) body(S2{}, t + 2);
+    if (t + 3 < KT) body(S3{}, t + 3);
+    if constexpr (STAGES > 4) {
+      if (t + 4 < KT) body(S4{}, t + 4);
+    }
+  }
+  // clamped tail loads may still be landing in LDS: drain before leaving
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+
+  // ---- epilogue, staged through the (now idle) LDS ring in two halves of
+  // 128 rows: waves of row-half h write t = bf16(acc) into padded rows
+  // (264 elements, so the two 32-lane row groups of a write hit opposite bank
+  // halves), then all 256 threads walk the half in 16-byte row chunks, apply
+  // bias / GELU / residual with vector loads and store 16 bytes at a time.
+  // 8-row block b of a half lives in ring array b / 3 at row offset (b % 3) * 8.
+  constexpr int EP_LD = 264;
+  auto ep_block = [&](int blk) -> uint16_t * {
+    switch (blk / 3) {
+      case 0: return As0 + (blk % 3) * 8 * EP_LD;
+      case 1: return As1 + (blk % 3) * 8 * EP_LD;
+      case 2: return As2 + (blk % 3) * 8 * EP_LD;
+      case 3: return As3 + (blk % 3) * 8 * EP_LD;
+      case 4: return (STAGES > 4 ? As4 : Bs1) + (blk % 3) * 8 * EP_LD;
+      default: return Bs0 + (blk % 3) * 8 * EP_LD;
+    }
+  };
+  __syncthreads();  // every wave is done reading the ring
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (wm == h) {
+#pragma unroll
+      for (int fm = 0; fm < 4; ++fm)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint16_t *blk = ep_block(fm * 4 + q);
+#pragma unroll
+          for (int fn = 0; fn < 4; ++fn) {
+            const int col = wn * 128 + fn * 32 + (lane & 31);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = (lane >> 5) * 4 + e;
+              blk[r * EP_LD + col] = (uint16_t)f2bf(acc[fm][fn][q * 4 + e]);
+            }
+          }
+        }
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) {
+      const int qd = tid + j * G2_THREADS;
+      const int r = qd >> 5, c = qd & 31;
+      const int m = m0 + h * 128 + r, n = n0 + 8 * c;
+      if (m < g.M && n < g.N) {
+        const uint16_t *src = ep_block(r >> 3) + (r & 7) * EP_LD + 8 * c;
+        const u32x4 tv = *reinterpret_cast<const u32x4 *>(src);
+        u32x4 ov;
+        if constexpr (EPI == EPI_NONE) {
+          ov = tv;
+        } else {
+          u32x4 bv = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
+          if constexpr (EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID)
+            if (g.bias) bv = *reinterpret_cast<const u32x4 *>(g.bias + n);
+          if constexpr (EPI == EPI_BIAS_RESID || EPI == EPI_RESID)
+            rv = *reinterpret_cast<const u32x4 *>(g.R + (size_t)m * g.N + n);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            uint32_t o2 = 0;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const float t = hh ? hi_bf(tv[w]) : lo_bf(tv[w]);
+              uint32_t o;
+              if constexpr (EPI == EPI_BIAS_GELU) {
+                o = gelu_bits(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))), g.gelu_tab);
+              } else if constexpr (EPI == EPI_BIAS_RESID) {
+                const float u = bf2f(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))));
+                o = f2bf(u + (hh ? hi_bf(rv[w]) : lo_bf(rv[w])));
+              } else {
+                o = f2bf(t + (hh ? hi_bf(rv[w]) : lo_bf(rv[w])));
+              }
+              o2 |= o << (16 * hh);
+            }
+            ov[w] = o2;
+          }
+        }
+        *reinterpret_cast<u32x4 *>(g.C + (size_t)m * g.N + n) = ov;
       }
     }
+    if (h == 0) __syncthreads();  // the half is consumed before the next overwrites it
   }
 }
 
@@ -271,9 +611,23 @@ int launch_tile(const GemmArgs &g, bool aligned, hipStream_t st) {
   return PK_OK;
 }
 
+// Ring depth of gemm_dma_kernel (tuning knob, see pk_gemm_set_ring_depth).
+int g_ring_depth = 5;
+
 template <int EPI>
 int gemm_dispatch(const GemmArgs &g, int tile, hipStream_t st) {
   const bool aligned = (g.K % 8 == 0) && (g.N % 8 == 0) && aligned16(g.A) && aligned16(g.B);
+  const bool offsets32 = (size_t)g.K * g.N * 2 < (size_t(1) << 31) &&
+                         (size_t)G2_BM * g.K * 2 < (size_t(1) << 31);
+  const bool ep_aligned = aligned16(g.C) && (!g.R || aligned16(g.R)) && (!g.bias || aligned16(g.bias));
+  if (tile == 0 && aligned && ep_aligned && offsets32 && g.K % G2_BK == 0 && g.N >= 8) {
+    const int tiles = ((g.M + G2_BM - 1) / G2_BM) * ((g.N + G2_BN - 1) / G2_BN);
+    if (g_ring_depth == 5) gemm_dma_kernel<EPI, 5><<<tiles, G2_THREADS, 0, st>>>(g);
+    else gemm_dma_kernel<EPI, 4><<<tiles, G2_THREADS, 0, st>>>(g);
+    PK_LAUNCH_CHECK("gemm_dma_kernel");
+    return PK_OK;
+  }
+  if (tile == 3) tile = 0;  // the 8-wave register-staged 256x256 kernel
   switch (tile) {
     case 0: return launch_tile<256, 256, 2, 4, EPI>(g, aligned, st);
     case 1: return launch_tile<128, 128, 2, 2, EPI>(g, aligned, st);
@@ -544,13 +898,22 @@ int launch_mlp_block(const uint16_t *x, const uint16_t *gamma, const uint16_t *W
   return gemm_run(EPI_BIAS_RESID, h, W2, out, b2, x, M, d, F, st);
 }
 
+// Tuning hook: LDS ring depth (4 or 5 k-tiles) of the DMA-pipelined GEMM.
+int pk_gemm_set_ring_depth(int depth) {
+  PK_CHECK_ARG(depth == 4 || depth == 5, "pk_gemm_set_ring_depth: depth must be 4 or 5");
+  g_ring_depth = depth;
+  return PK_OK;
+}
+
 // Test/tuning hook: run one GEMM epilogue variant with an explicit tile choice
-// (0: 256x256, 1: 128x128, 2: 64x64; -1: heuristic).
+// (0: 256x256 -- the DMA-pipelined kernel when K % 32 == 0 and the operands
+// are aligned, 1: 128x128, 2: 64x64, 3: the register-staged 256x256 kernel;
+// -1: heuristic).
 int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
                const uint16_t *R, int M, int N, int K, int tile, void *stream) {
   PK_CHECK_ARG(A && B && C, "pk_gemm_ex: null tensor pointer");
   PK_CHECK_ARG(M > 0 && N > 0 && K > 0, "pk_gemm_ex: invalid shape");
-  PK_CHECK_ARG(epi >= 0 && epi <= 3 && tile >= -1 && tile <= 2, "pk_gemm_ex: bad epi/tile");
+  PK_CHECK_ARG(epi >= 0 && epi <= 3 && tile >= -1 && tile <= 3, "pk_gemm_ex: bad epi/tile");
   return gemm_run(epi, A, B, C, bias, R, M, N, K, (hipStream_t)stream, tile);
 }
 

@@ -71,7 +71,7 @@ __device__ __forceinline__ uint16_t int8_epilogue(float dot, int m, int n, const
   if constexpr (EPI == I8_NONE) {
     return (uint16_t)t;
   } else if constexpr (EPI == I8_GELU) {
-    return g.gelu_tab[t];
+    return (uint16_t)gelu_bits(t, g.gelu_tab);
   } else {
     return (uint16_t)f2bf(bf2f(t) + bf2f(g.R[(size_t)m * g.N + n]));
   }

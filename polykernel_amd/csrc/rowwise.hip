@@ -320,7 +320,7 @@ int softmax_dispatch(const void *in, const uint16_t *mask, uint16_t *y, int rows
 }
 
 // ---------------------------------------------------------------------------
-// GELU by table: out = table[in]  (table built from kernels/cpu/cpu_reference.cpp:46-55).
+// GELU: out = gelu_bits(in)  (kernels/cpu/cpu_reference.cpp:46-55, exact).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kBlock) void gelu_kernel(const uint16_t *__restrict__ in,
                                                       uint16_t *__restrict__ out, int64_t n,
@@ -332,18 +332,19 @@ __global__ __launch_bounds__(kBlock) void gelu_kernel(const uint16_t *__restrict
     uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      w[j] = (uint32_t)tab[w[j] & 0xFFFFu] | ((uint32_t)tab[w[j] >> 16] << 16);
+      w[j] = gelu_bits(w[j] & 0xFFFFu, tab) | (gelu_bits(w[j] >> 16, tab) << 16);
     st16(out + v * 8, U4{w[0], w[1], w[2], w[3]});
   }
   for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
-    out[i] = tab[in[i]];
+    out[i] = (uint16_t)gelu_bits(in[i], tab);
 }
 
 __global__ __launch_bounds__(kBlock) void gelu_scalar_kernel(const uint16_t *__restrict__ in,
                                                              uint16_t *__restrict__ out, int64_t n,
                                                              const uint16_t *__restrict__ tab) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) out[i] = tab[in[i]];
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+    out[i] = (uint16_t)gelu_bits(in[i], tab);
 }
 
 // ---------------------------------------------------------------------------

@@ -57,6 +57,17 @@ def _abs_dot(a_bits, b_bits):
 
 # ------------------------------------------------------------------ elementwise / rows
 
+def test_device_bf16_conversion_exhaustive(gpu):
+    """All 2^32 fp32 inputs: the kernels' hardware fp32->bf16 conversion equals
+    the reference RNE formula (kernels/cpu/cpu_reference.h:52-61)."""
+    import ctypes
+    from polykernel_amd import _lib
+
+    bad = ctypes.c_ulonglong(123)
+    _lib.check(_lib.load().pk_check_bf16_conversion(ctypes.byref(bad)), "pk_check_bf16_conversion")
+    assert bad.value == 0
+
+
 def test_gelu_all_bf16_codes_bit_exact(gpu, oracle):
     x = np.arange(1 << 16, dtype=np.uint16)
     got = from_dev(K().gelu(to_dev(x)))
@@ -145,8 +156,9 @@ def test_quantize_ties_bit_exact(gpu, oracle):
 
 # ------------------------------------------------------------------ GEMM family
 
-@pytest.mark.parametrize("tile", [0, 1, 2])
-@pytest.mark.parametrize("M,N,Kd", [(256, 256, 512), (130, 65, 127), (300, 520, 200)])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+@pytest.mark.parametrize("M,N,Kd", [(256, 256, 512), (130, 65, 127), (300, 520, 200), (300, 520, 224),
+                                    (513, 264, 32), (1024, 768, 1056)])
 def test_gemm_integer_inputs_bit_exact(gpu, oracle, tile, M, N, Kd):
     _say(f"gemm int tile={tile} {M}x{N}x{Kd}")
     a, b = int_bf16((M, Kd), 14), int_bf16((Kd, N), 15)
@@ -159,7 +171,8 @@ def test_matmul_known_2x2(gpu):
     assert np.array_equal(got, np.array([[19, 22], [43, 50]], np.float32))
 
 
-@pytest.mark.parametrize("M,N,Kd", [(128, 3072, 768), (130, 65, 127), (512, 1024, 4096), (64, 64, 64)])
+@pytest.mark.parametrize("M,N,Kd", [(128, 3072, 768), (130, 65, 127), (512, 1024, 4096), (64, 64, 64),
+                                    (1024, 2048, 2048)])
 def test_matmul_random(gpu, oracle, M, N, Kd):
     _say(f"matmul {M}x{N}x{Kd}")
     a = synth.normal_bf16((M, Kd), 16)
@@ -210,17 +223,21 @@ def test_fused_matmul_bias_gelu(gpu, oracle, M, N, Kd):
     assert rep.bit_exact >= 0.95, rep
 
 
-def test_fused_matmul_bias_gelu_integer_bit_exact(gpu, oracle):
-    a, b = int_bf16((256, 384), 29), int_bf16((384, 512), 30)
-    bias = bf(np.random.default_rng(31).integers(-4, 5, size=512))
-    got = from_dev(K().fused_matmul_bias_gelu(to_dev(a), to_dev(b), to_dev(bias)))
+@pytest.mark.parametrize("tile", [0, 3])
+def test_fused_matmul_bias_gelu_integer_bit_exact(gpu, oracle, tile):
+    a, b = int_bf16((600, 384), 29), int_bf16((384, 520), 30)
+    bias = bf(np.random.default_rng(31).integers(-4, 5, size=520))
+    got = from_dev(K().gemm_ex(1, to_dev(a), to_dev(b), bias=to_dev(bias), tile=tile))
     assert np.array_equal(got, oracle.fused_matmul_bias_gelu(a, b, bias))
 
 
-def test_fused_matmul_bias_residual_integer_bit_exact(gpu, oracle):
-    a, b = int_bf16((256, 384), 32), int_bf16((384, 512), 33)
-    bias = bf(np.random.default_rng(34).integers(-4, 5, size=512))
-    r = rng_bf16((256, 512), 35)
+@pytest.mark.parametrize("tile", [0, 3])
+def test_fused_matmul_bias_residual_integer_bit_exact(gpu, oracle, tile):
+    a, b = int_bf16((600, 384), 32), int_bf16((384, 520), 33)
+    bias = bf(np.random.default_rng(34).integers(-4, 5, size=520))
+    r = rng_bf16((600, 520), 35)
+    got = from_dev(K().gemm_ex(2, to_dev(a), to_dev(b), bias=to_dev(bias), residual=to_dev(r), tile=tile))
+    assert np.array_equal(got, oracle.fused_matmul_bias_residual(a, b, bias, r))
     got = from_dev(K().fused_matmul_bias_residual(to_dev(a), to_dev(b), to_dev(bias), to_dev(r)))
     assert np.array_equal(got, oracle.fused_matmul_bias_residual(a, b, bias, r))
     got = from_dev(K().fused_matmul_bias_residual(to_dev(a), to_dev(b), None, to_dev(r)))
