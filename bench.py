@@ -339,7 +339,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": read_traffic(),
-                     "kernel": "gemm_kernel<256,256,2,4,EPI_BIAS_GELU> (GEMM1, 2^39 FLOP/launch)"},
+                     "kernel": "gemm_dma_kernel<EPI_BIAS_GELU,5> (GEMM1: x@W1+b1->GELU, 2^39 FLOP/launch)"},
         "cpu_baseline": cpu,
         "extra": extra,
     }
