@@ -208,12 +208,23 @@ def bench_extra(reps: int = 20):
     torch.cuda.empty_cache()
     ws = torch.empty(lib.pk_decode_mlp_int8_workspace_size(Md, dd, Fd), dtype=torch.uint8, device="cuda")
     od = torch.empty_like(xd)
-    ms = timeit(lambda: check(lib.launch_decode_mlp_int8(
-        xd.data_ptr(), w1q.data_ptr(), s1.data_ptr(), w2q.data_ptr(), s2.data_ptr(), od.data_ptr(),
-        Md, dd, Fd, ws.data_ptr(), ws.numel(), sp), "cfg5"))
+    # two copies of the weights, used in turn: 940 MB, so the 256 MB MALL
+    # holds none of a call's weights when it starts
+    wsets = [(w1q, w2q), (w1q.clone(), w2q.clone())]
+    turn = [0]
+
+    def decode():
+        a, b = wsets[turn[0] % 2]
+        turn[0] += 1
+        check(lib.launch_decode_mlp_int8(
+            xd.data_ptr(), a.data_ptr(), s1.data_ptr(), b.data_ptr(), s2.data_ptr(), od.data_ptr(),
+            Md, dd, Fd, ws.data_ptr(), ws.numel(), sp), "cfg5")
+
+    ms = timeit(decode)
     gbs = 470433792 / (ms * 1e-3) / 1e9
     out["int8_decode_mlp_cfg5"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
-                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                   "note": "2 weight copies in turn (no MALL reuse)"}
     return out
 
 

@@ -176,6 +176,33 @@ PK_API int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C
  * 5 uses all 160 KiB of LDS).  Process-wide; default 5. */
 PK_API int pk_gemm_set_ring_depth(int depth);
 
+/* Launch configuration of the streaming int8 kernel (the fast path of
+ * launch_matmul_int8 when N % 16 == 0, K % 64 == 0 and A, Wq, scale, C are
+ * 16-byte aligned).  Field names follow the tuning-cache config
+ * (tuning/schema.json:65-79): block_n = output columns per workgroup, split
+ * over num_warps waves of 16..256 columns each (see the variant table in
+ * int8.hip); block_k = rows of K one workgroup reduces (a multiple of 64;
+ * K / block_k workgroups per column slice, their fp32 partials summed by a
+ * second kernel); shared_memory_stages = per-wave LDS ring depth in 64-row
+ * steps; block_m = rows of A per workgroup (16, 32 or 64).  0 in any field
+ * selects the built-in choice for it. */
+typedef struct pk_int8_config {
+  int block_m, block_n, block_k, num_warps, shared_memory_stages;
+} pk_int8_config;
+
+/* The configuration launch_matmul_int8 would use for this shape (returns
+ * PK_ERR_UNSUPPORTED when the shape takes the generic kernel). */
+PK_API int pk_int8_default_config(int M, int N, int K, pk_int8_config *out);
+
+/* Tuning/test hook: int8 matmul with an explicit epilogue (0 none, 1 GELU,
+ * 2 residual add of R [M,N]) and configuration (NULL = built-in choice).
+ * Unsupported configurations return PK_ERR_UNSUPPORTED.  `workspace` (may be
+ * NULL: library-owned) holds the split partials. */
+PK_API int pk_matmul_int8_ex(int epi, const uint16_t *A, const int8_t *Wq, const float *scale,
+                             uint16_t *C, const uint16_t *R, int M, int N, int K,
+                             const pk_int8_config *cfg, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
 /* ---- synthetic inputs (host, deterministic, OpenMP) -------------------- */
 
 /* out[i] = bf16 RNE of float(mean + std * z_i), z_i standard normal from the

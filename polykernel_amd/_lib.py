@@ -30,6 +30,16 @@ class PolyKernelError(RuntimeError):
         self.message = message
 
 
+class Int8Config(C.Structure):
+    """struct pk_int8_config (include/polykernel_amd.h); 0 = built-in choice."""
+
+    _fields_ = [("block_m", C.c_int), ("block_n", C.c_int), ("block_k", C.c_int),
+                ("num_warps", C.c_int), ("shared_memory_stages", C.c_int)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 P = C.c_void_p
 I = C.c_int
 F = C.c_float
@@ -67,6 +77,8 @@ SIGNATURES = {
     "launch_decode_mlp_int8": (I, [P, P, P, P, P, P, I, I, I, P, SZ, P]),
     "pk_gemm_ex": (I, [I, P, P, P, P, P, I, I, I, I, P]),
     "pk_gemm_set_ring_depth": (I, [I]),
+    "pk_int8_default_config": (I, [I, I, I, C.POINTER(Int8Config)]),
+    "pk_matmul_int8_ex": (I, [I, P, P, P, P, P, I, I, I, C.POINTER(Int8Config), P, SZ, P]),
     "pk_synth_normal_bf16": (None, [U64, U64, D, D, P, I64]),
     "pk_synth_normal_f32": (None, [U64, U64, D, D, P, I64]),
     "pk_synth_mask_bf16": (None, [U64, U64, D, P, I64]),

@@ -298,13 +298,7 @@ constexpr int G2_BM = 256, G2_BN = 256, G2_BK = 32, G2_STAGES = 4;
 constexpr int G2_THREADS = 256;
 constexpr int G2_DMA_PER_TILE = 8;  // 1 KiB global_load_lds per wave per tile: 4 for A, 4 for B
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 __device__ __forceinline__ int swz_a32(int row) { return (row >> 1) & 3; }
-
-// s_waitcnt immediate (gfx9 encoding): vmcnt in bits [3:0] and [15:14],
-// expcnt [6:4], lgkmcnt [11:8]; expcnt and lgkmcnt left at "no wait".
-constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
 
 __device__ __forceinline__ void vm_wait(int n_tiles) {
   // wait until at most n_tiles * G2_DMA_PER_TILE of this wave's DMA loads are in flight

@@ -114,6 +114,60 @@ __device__ __forceinline__ uint32_t gelu_bits(uint32_t u, const uint16_t *__rest
   return neg ? 0x8000u : u;
 }
 
+// ---- direct-to-LDS loads ----------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt in bits [3:0] and [15:14],
+// expcnt [6:4], lgkmcnt [11:8]; expcnt and lgkmcnt left at "no wait".
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+// lgkmcnt(0), vmcnt and expcnt left at "no wait".
+constexpr int WAITCNT_LGKM0 = 0xC07F;
+
+// Buffer resource over [base, base + bytes): loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// The same resource as four words for inline asm: base address, stride 0,
+// num_records, raw-dword access flags.  The arguments must be wave-uniform;
+// readfirstlane makes that visible to the compiler so the words live in SGPRs.
+typedef uint32_t pk_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ pk_u32x4 rsrc_words(const void *base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  return pk_u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xFFFFu)),
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000u};
+}
+
+// buffer_load_dwordx4 ... lds: lane i copies 16 bytes from rsrc + voff + soff
+// to LDS address lds + 16 * i.  Issued as inline asm so that the compiler's
+// wait-count pass does not track it: at loop headers that pass merges its
+// per-array record of pending LDS DMA into "any array" and then waits for
+// every pending load before the next LDS read, draining a ring each
+// iteration.  Callers order these loads with vm_wait<N>() themselves.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_lds16(pk_u32x4 rsrc, const void *lds, uint32_t voff, uint32_t soff) {
+  // lds and soff are wave-uniform; readfirstlane keeps them in SGPRs (the
+  // "s" constraint does not move a VGPR value by itself)
+  const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)reinterpret_cast<uintptr_t>((lds_void *)lds));
+  const int so = __builtin_amdgcn_readfirstlane((int)soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until at most N of this wave's vector-memory loads are outstanding
+// (loads complete in issue order); a compiler memory barrier as well.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lgkm_wait0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll

@@ -239,6 +239,31 @@ def matmul_int8(a: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor) -> torch
     return out
 
 
+def int8_default_config(M: int, N: int, K: int) -> Optional[dict]:
+    """Configuration launch_matmul_int8 picks for a shape (None: generic kernel)."""
+    cfg = _lib.Int8Config()
+    rc = _lib.load().pk_int8_default_config(M, N, K, cfg)
+    if rc == _lib.PK_ERR_UNSUPPORTED:
+        return None
+    check(rc, "pk_int8_default_config")
+    return cfg.as_dict()
+
+
+def matmul_int8_ex(epi: int, a: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
+                   residual: Optional[torch.Tensor] = None, config: Optional[dict] = None) -> torch.Tensor:
+    """int8 matmul with an explicit epilogue (0 none, 1 GELU, 2 + residual) and
+    launch configuration (tuning/test hook pk_matmul_int8_ex)."""
+    K = a.shape[-1]
+    M, N = a.numel() // K, wq.shape[1]
+    out = torch.empty(*a.shape[:-1], N, dtype=bf16, device=a.device)
+    cfg = None if config is None else _lib.Int8Config(**config)
+    check(_lib.load().pk_matmul_int8_ex(epi, _dev(a, bf16, "a"), _dev(wq, torch.int8, "wq"),
+                                        _dev(scale, torch.float32, "scale"), _dev(out, bf16, "out"),
+                                        _opt(residual, bf16, "residual"), M, N, K, cfg, None, 0,
+                                        _stream()), "pk_matmul_int8_ex")
+    return out
+
+
 def decode_mlp_int8(x, w1q, s1, w2q, s2, workspace: Optional[torch.Tensor] = None):
     """add(matmul_int8(gelu(matmul_int8(x, W1q, s1)), W2q, s2), x) (config-5 chain)."""
     d = x.shape[-1]

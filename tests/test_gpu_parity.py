@@ -301,6 +301,78 @@ def test_matmul_int8_integer_bit_exact(gpu, oracle):
     assert np.array_equal(got, oracle.matmul_int8(a, wq, s))
 
 
+# Variants of the streaming int8 kernel (block_m, block_n, num_warps, stages):
+# every instantiation the library carries (block_n = 16 * NT * waves).
+_I8S_VARIANTS = [(16, 512, 4, 3), (16, 448, 4, 3), (16, 256, 2, 6), (16, 256, 4, 6), (16, 512, 8, 3),
+                 (16, 512, 2, 4), (16, 128, 4, 6), (16, 64, 4, 6), (16, 448, 4, 4),
+                 (32, 512, 4, 3), (32, 256, 4, 4), (32, 128, 4, 6),
+                 (64, 512, 4, 2), (64, 256, 4, 3), (64, 128, 4, 3)]
+
+
+def _int8_exact_inputs(M, N, Kd, seed):
+    """Integer-valued activations, int8 weights, power-of-two scales: every
+    partial sum is an integer below 2^24, so any summation order is exact and
+    the GPU must match the oracle bit for bit."""
+    a = int_bf16((M, Kd), seed, -4, 4)
+    r = np.random.default_rng(seed + 1)
+    wq = r.integers(-127, 128, size=(Kd, N)).astype(np.int8)
+    s = (2.0 ** r.integers(-9, -4, size=N)).astype(np.float32)
+    return a, wq, s
+
+
+@pytest.mark.parametrize("bm,bn,waves,stages", _I8S_VARIANTS)
+@pytest.mark.parametrize("block_k", [0, 192, 1024])
+def test_matmul_int8_stream_variants_bit_exact(gpu, oracle, bm, bn, waves, stages, block_k):
+    """Each variant, with the built-in K split and explicit ones (192 rows: 3
+    steps, fewer than the ring depth; 1024 rows); N leaves a ragged last slice
+    (and whole waves past N), M a ragged last m-tile."""
+    M, N, Kd = bm - 3, 2 * bn + bn // 4 + 16, 1600 - 1600 % 64
+    cfg = dict(block_m=bm, block_n=bn, block_k=block_k, num_warps=waves, shared_memory_stages=stages)
+    _say(f"int8 stream {cfg} M={M} N={N} K={Kd}")
+    a, wq, s = _int8_exact_inputs(M, N, Kd, 70)
+    got = from_dev(K().matmul_int8_ex(0, to_dev(a), to_dev(wq), to_dev(s), config=cfg))
+    assert np.array_equal(got, oracle.matmul_int8(a, wq, s))
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 16, 64), (5, 112, 64), (16, 1024, 128), (17, 2048, 4096),
+                                    (64, 4096, 1024), (65, 256, 512), (130, 512, 256),
+                                    (16, 28672, 512), (16, 8192, 1024)])
+def test_matmul_int8_default_config_bit_exact(gpu, oracle, M, N, Kd):
+    cfg = K().int8_default_config(M, N, Kd)
+    _say(f"int8 default {M}x{N}x{Kd}: {cfg}")
+    assert cfg is not None
+    a, wq, s = _int8_exact_inputs(M, N, Kd, 71)
+    got = from_dev(K().matmul_int8(to_dev(a), to_dev(wq), to_dev(s)))
+    assert np.array_equal(got, oracle.matmul_int8(a, wq, s))
+
+
+@pytest.mark.parametrize("cfg", [None, dict(block_m=16, block_n=256, block_k=256, num_warps=4,
+                                            shared_memory_stages=6)])
+def test_matmul_int8_epilogues_bit_exact(gpu, oracle, cfg):
+    """GELU and residual epilogues, direct and through the split reduction."""
+    M, N, Kd = 16, 1024, 1024
+    a, wq, s = _int8_exact_inputs(M, N, Kd, 72)
+    r = rng_bf16((M, N), 73)
+    plain = oracle.matmul_int8(a, wq, s)
+    got_g = from_dev(K().matmul_int8_ex(1, to_dev(a), to_dev(wq), to_dev(s), config=cfg))
+    assert np.array_equal(got_g, oracle.gelu(plain))
+    got_r = from_dev(K().matmul_int8_ex(2, to_dev(a), to_dev(wq), to_dev(s), residual=to_dev(r),
+                                        config=cfg))
+    assert np.array_equal(got_r, oracle.add(plain, r))
+
+
+def test_matmul_int8_unsupported_config(gpu):
+    from polykernel_amd._lib import PK_ERR_UNSUPPORTED, PolyKernelError
+
+    a = to_dev(int_bf16((16, 256), 74))
+    wq = to_dev(np.zeros((256, 192), np.int8))
+    s = to_dev(np.ones(192, np.float32))
+    for cfg in (dict(block_n=96), dict(block_n=1024), dict(block_k=100), dict(block_m=48), dict(num_warps=3)):
+        with pytest.raises(PolyKernelError) as e:
+            K().matmul_int8_ex(0, a, wq, s, config=cfg)
+        assert e.value.code == PK_ERR_UNSUPPORTED
+
+
 def test_decode_mlp_int8_config5(gpu, oracle):
     M, d, F = 16, 8192, 28672
     _say("decode int8 config5")
