@@ -284,13 +284,16 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
 // Large-tile GEMM (the MLP block path).  256x256 per workgroup, 4 waves in a
 // 2x2 grid, each wave owning a 128x128 sub-tile (16 MFMA accumulator blocks,
 // 256 fp32 per lane, held in AGPRs).  K advances in tiles of 32 through a
-// 4-stage LDS ring filled by global_load_lds_dwordx4 (global -> LDS without
-// VGPR staging) issued three tiles ahead.  Per k-tile and wave:
-//     read B/A fragments of substep 1 | MFMAs of substep 0 |
-//     wait own DMA of tile t+1, s_barrier, DMA tile t+4 into the freed stage |
-//     read fragments of tile t+1 substep 0 | MFMAs of substep 1
+// STAGES-deep LDS ring (4 or 5) filled by buffer_load_dwordx4 ... lds
+// (global -> LDS without VGPR staging) issued STAGES-1 tiles ahead.  Per
+// k-tile and wave:
+//     MFMAs of substep 0, interleaved with the fragment reads of substep 1 |
+//     wait own reads and own DMA of tile t+1, s_barrier |
+//     MFMAs of substep 1, interleaved with the DMA of tile t+STAGES into the
+//     freed stage and the fragment reads of tile t+1 substep 0
 // so the single barrier sits behind queued MFMA work and every LDS read is
-// issued one substep before its use.  Requires K % 32 == 0, N % 8 == 0 and
+// issued one substep before its use.  The DMA is issued as inline asm
+// (dma_lds16) and ordered only by the explicit waits below.  Requires K % 32 == 0, N % 8 == 0 and
 // 16-byte aligned A/B; out-of-range rows/columns are clamped to valid memory
 // (their results are never stored).
 // ---------------------------------------------------------------------------
@@ -299,14 +302,6 @@ constexpr int G2_THREADS = 256;
 constexpr int G2_DMA_PER_TILE = 8;  // 1 KiB global_load_lds per wave per tile: 4 for A, 4 for B
 
 __device__ __forceinline__ int swz_a32(int row) { return (row >> 1) & 3; }
-
-__device__ __forceinline__ void vm_wait(int n_tiles) {
-  // wait until at most n_tiles * G2_DMA_PER_TILE of this wave's DMA loads are in flight
-  if (n_tiles >= 3) __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * G2_DMA_PER_TILE));
-  else if (n_tiles == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * G2_DMA_PER_TILE));
-  else if (n_tiles == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(G2_DMA_PER_TILE));
-  else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-}
 
 template <int EPI, int STAGES>
 __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
@@ -369,18 +364,13 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
     const int cc = min(8 * c, g.N - 8 - n0);
     b_off[j] = (uint32_t)(r * g.N + cc) * 2u;
   }
-  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(g.A + (size_t)m0 * g.K), (short)0, (g.M - m0) * g.K * 2, 0x00020000);
-  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(g.B + n0), (short)0, (g.K * g.N - n0) * 2, 0x00020000);
-  auto issue_one = [&](auto c, int t, int j) {
+  const pk_u32x4 a_rsrc = rsrc_words(g.A + (size_t)m0 * g.K, (uint32_t)((size_t)(g.M - m0) * g.K * 2));
+  const pk_u32x4 b_rsrc = rsrc_words(g.B + n0, (uint32_t)(((size_t)g.K * g.N - n0) * 2));
+  auto issue_one = [&](auto c, int t, int j) __attribute__((always_inline)) {
     if (j < 4)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)&a_stage(c)[(64 * wid + 16 * j) * G2_BK],
-                                               16, a_off[j], t * (G2_BK * 2), 0, 0);
+      dma_lds16(a_rsrc, &a_stage(c)[(64 * wid + 16 * j) * G2_BK], a_off[j], t * (G2_BK * 2));
     else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc,
-                                               (lds_void *)&b_stage(c)[(8 * wid + 2 * (j - 4)) * G2_BN], 16,
-                                               b_off[j - 4], t * (G2_BK * 2) * g.N, 0, 0);
+      dma_lds16(b_rsrc, &b_stage(c)[(8 * wid + 2 * (j - 4)) * G2_BN], b_off[j - 4], t * (G2_BK * 2) * g.N);
   };
   auto issue = [&](auto c, int t) {
 #pragma unroll
@@ -464,8 +454,9 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   issue(S2{}, min(2, KT - 1));
   issue(S3{}, min(3, KT - 1));
   if constexpr (STAGES > 4) issue(S4{}, min(4, KT - 1));
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * G2_DMA_PER_TILE));
+  vm_wait<(STAGES - 1) * G2_DMA_PER_TILE>();
   __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");  // no LDS access moves above the barrier
   __builtin_amdgcn_sched_barrier(0);
 
   Frag f0, f1;
@@ -487,9 +478,10 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
     }
     // this wave's reads of stage st are done and its DMA of tile t+1 landed
     // (STAGES-2 newer tiles may still be in flight); then all waves agree.
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * G2_DMA_PER_TILE));
+    lgkm_wait0();
+    vm_wait<(STAGES - 2) * G2_DMA_PER_TILE>();
     __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // no LDS access moves above the barrier
     __builtin_amdgcn_sched_barrier(0);
     const int tn_dma = min(t + STAGES, KT - 1);
 #pragma unroll
@@ -510,7 +502,7 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
     }
   }
   // clamped tail loads may still be landing in LDS: drain before leaving
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  vm_wait<0>();
 
   // ---- epilogue, staged through the (now idle) LDS ring in two halves of
   // 128 rows: waves of row-half h write t = bf16(acc) into padded rows

@@ -103,15 +103,21 @@ __device__ __forceinline__ uint32_t gelu_table_code(int i) {
   return i < GELU_NPOS ? GELU_TLO + (uint32_t)i : 0x8000u | (GELU_TLO + (uint32_t)(i - GELU_NPOS));
 }
 
+// Branch-free: the table is read at a clamped index for every input (always
+// in bounds) and the rules are selects, so a wave never splits on the input.
 __device__ __forceinline__ uint32_t gelu_bits(uint32_t u, const uint16_t *__restrict__ tab) {
   const uint32_t mag = u & 0x7FFFu;
   const bool neg = (u & 0x8000u) != 0u;
-  const uint32_t hi = neg ? GELU_NHI : GELU_PHI;
-  if (mag >= GELU_TLO && mag <= hi) return tab[(neg ? GELU_NPOS : 0) + (int)(mag - GELU_TLO)];
-  if (mag > 0x7F80u) return u | 0x0040u;
-  if (u == 0xFF80u) return 0xFFC0u;
-  if (mag < GELU_TLO) return f2bf(0.5f * bf2f(u));
-  return neg ? 0x8000u : u;
+  const uint32_t off = mag - GELU_TLO;  // wraps for mag < TLO
+  const bool in_tab = off <= (neg ? GELU_NHI - GELU_TLO : GELU_PHI - GELU_TLO);
+  const uint32_t idx = in_tab ? (neg ? (uint32_t)GELU_NPOS : 0u) + off : 0u;
+  const uint32_t tv = tab[idx];
+  const uint32_t half = f2bf(0.5f * bf2f(u));
+  uint32_t r = neg ? 0x8000u : u;        // |x| above the table: x or -0
+  r = mag < GELU_TLO ? half : r;         // |x| below the table: 0.5 x
+  r = u == 0xFF80u ? 0xFFC0u : r;        // -inf
+  r = mag > 0x7F80u ? (u | 0x0040u) : r; // NaN -> quiet NaN
+  return in_tab ? tv : r;
 }
 
 // ---- direct-to-LDS loads ----------------------------------------------------
