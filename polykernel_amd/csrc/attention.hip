@@ -19,10 +19,11 @@
 // that key order, so P never leaves registers and the rescale by
 // exp(m_old - m_new) is a per-lane multiply.
 //
-// Work split: a workgroup = 4 waves x 32 queries of one (b,h); K/V tiles are
-// double-buffered in LDS.  When queries alone do not fill the chip the key
-// range is split (flash-decoding style) and att_combine_kernel merges the
-// fp32 partials in split order.
+// Work split (attention_kernel, any D <= 128): a workgroup = 4 waves x 32
+// queries of one (b,h); K/V tiles are double-buffered in LDS.  When queries
+// alone do not fill the chip the key range is split (flash-decoding style)
+// and att_combine_kernel merges the fp32 partials in split order.  Head dims
+// 64 and 128 with enough query tiles take attention_fa_kernel (below).
 #include "pk_common.hpp"
 
 namespace pk {
@@ -32,6 +33,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -329,6 +331,380 @@ __global__ __launch_bounds__(256) void att_combine_kernel(AttArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Flash-style prefill for head dims 64 and 128 (the config-3 path).
+//
+// A workgroup of 8 waves owns 32*QG queries of one (b,h) and walks its key
+// range in steps of 32*KH keys (QG * KH = 8): wave (qg, kh) handles query
+// group qg (32 queries, the S^T layout above) against keys
+// [step*32*KH + 32*kh, +32) with its own running max / sum / accumulator.
+// Two waves share each SIMD, so one can run the softmax while the other
+// issues MFMAs.  K and V tiles arrive in a ring of LDS stages by
+// buffer_load ... lds (waves 0-3 load K, 4-7 V), one barrier per step; the
+// ring holds 128 KiB, i.e. STAGES-1 steps of prefetch.  Diagonal blocks are
+// masked, blocks above the diagonal skipped.  At the end the KH partial
+// states of each query are merged in LDS in kh order.  When the grid would
+// not fill the chip, the key range is also split over `splits` workgroups
+// whose fp32 partials fa_combine_kernel merges in split order.
+// Fused KV append: rows >= S_cache are read from K_new/V_new directly and the
+// kernel also copies them into the cache (no reader of the cache needs them,
+// so the copy is unordered).
+constexpr int FA_WAVES = 8;
+constexpr int FA_THREADS = FA_WAVES * 64;
+constexpr int FA_RING = 128 * 1024;  // bytes of LDS ring
+
+struct FaArgs {
+  const uint16_t *Q;
+  const uint16_t *K, *V;    // rows [0, S_cache) of each head, row stride D, head stride kv_rows
+  const uint16_t *Kn, *Vn;  // fused append: rows [S_cache, S_kv) of each head (else null)
+  uint16_t *Kc, *Vc;        // fused append: cache the new rows are copied into
+  uint16_t *O;
+  float *part_o;            // splits > 1: [splits][BH*S_q][DP] unnormalised
+  float *part_ml;           // splits > 1: [splits][BH*S_q][2] (max, sum)
+  int BH, S_q, S_kv, S_cache, kv_rows;
+  float scale;
+  int causal;
+  int q_tiles, splits;
+};
+
+template <int DP, int QG, bool FUSED>
+__global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
+  constexpr int KH = FA_WAVES / QG;          // key blocks of 32 per step
+  constexpr int BQ = 32 * QG;                // queries per workgroup
+  constexpr int BKV = 32 * KH;               // keys per step
+  constexpr int CH = DP / 8;                 // 16-byte chunks per row
+  constexpr int TB = BKV * DP * 2;           // bytes of one K (or V) tile
+  constexpr int STAGES = FA_RING / (2 * TB);
+  constexpr int NK = TB / 1024;              // DMA instructions per tile
+  constexpr int NPW = NK / (FA_WAVES / 2);   // per wave per step
+  constexpr int RPI = 1024 / (2 * DP);       // rows per DMA instruction
+  constexpr int DS = DP / 16, DB = DP / 32;
+  static_assert(STAGES >= 2 && NPW >= 1 && NK % (FA_WAVES / 2) == 0, "ring shape");
+  constexpr int PS = DP + 4;                 // merge-buffer row stride (floats), 16 B padding
+  constexpr int MERGE = FA_WAVES * 32 * PS * 4;
+  // the ring, reused as the merge buffer after the last step
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[MERGE > FA_RING ? MERGE : FA_RING];
+  __shared__ float ml_s[FA_WAVES][32][2];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = wid % QG, kh = wid / QG;
+  // arguments used in the loop, read once
+  const float scale = g.scale;
+  const bool causal = g.causal != 0;
+  const int S_cache = g.S_cache;
+  const int h = lane >> 5, grp = lane >> 4, gi = lane & 15;
+  int b = blockIdx.x;
+  const int per_bh = g.q_tiles * g.splits;
+  const int total = g.BH * per_bh;
+  if ((total & 7) == 0) b = (b & 7) * (total >> 3) + (b >> 3);
+  const int bh = b / per_bh, rem = b % per_bh;
+  const int qt = rem / g.splits, split = rem % g.splits;
+  const int q0 = qt * BQ;
+  const int qw = q0 + 32 * qg;
+  const int my_q = qw + (lane & 31);
+  const int off = g.S_kv - g.S_q;
+  const int kv_end = causal ? min(g.S_kv, max(0, off + q0 + BQ)) : g.S_kv;
+  const int ntiles = (kv_end + BKV - 1) / BKV;
+  const int tps = (ntiles + g.splits - 1) / g.splits;
+  const int t_begin = min(ntiles, split * tps);
+  const int nsteps = min(ntiles, t_begin + tps) - t_begin;
+  const int S_new = g.S_kv - S_cache;
+
+  // ---- fused append: this workgroup's share of the new rows -> cache
+  if (FUSED) {
+    const int64_t per_head = (int64_t)S_new * DP / 8;  // 16-byte units
+    const int64_t units = (int64_t)g.BH * per_head;
+    for (int64_t u = (int64_t)blockIdx.x * FA_THREADS + tid; u < units; u += (int64_t)gridDim.x * FA_THREADS) {
+      const int64_t hd = u / per_head, r = u % per_head;
+      const size_t src = (size_t)hd * S_new * DP + (size_t)r * 8;
+      const size_t dst = ((size_t)hd * g.kv_rows + S_cache) * DP + (size_t)r * 8;
+      *reinterpret_cast<u32x4 *>(g.Kc + dst) = *reinterpret_cast<const u32x4 *>(g.Kn + src);
+      *reinterpret_cast<u32x4 *>(g.Vc + dst) = *reinterpret_cast<const u32x4 *>(g.Vn + src);
+    }
+  }
+
+  // ---- Q^T fragments (B operand): query lane % 32, d = 16 ds + 8 h + 0..7
+  bf16x8 qf[DS];
+  {
+    const uint16_t *qrow = g.Q + ((size_t)bh * g.S_q + min(my_q, g.S_q - 1)) * DP;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      u32x4 v = *reinterpret_cast<const u32x4 *>(qrow + 16 * ds + 8 * h);
+      if (my_q >= g.S_q) v = u32x4{0, 0, 0, 0};
+      qf[ds] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  // ---- DMA: per head, the cache rows and (FUSED) the new rows; with FUSED,
+  // S_cache is a multiple of BKV, so a step reads one source.  Waves 0-3 load
+  // the K tile, waves 4-7 the V tile, NPW 1 KiB instructions each;
+  // instruction qq covers tile rows qq*RPI .. qq*RPI+RPI-1.  The per-lane
+  // offset inside the tile is loop-invariant and the step's first row goes
+  // into the scalar offset; only a step that reaches past kv_end clamps rows
+  // (onto the last visible row: finite data, masked).
+  const bool isk = wid < FA_WAVES / 2;
+  const int wq = isk ? wid : wid - FA_WAVES / 2;
+  const uint16_t *src_c = (isk ? g.K : g.V) + (size_t)bh * g.kv_rows * DP;
+  const uint16_t *src_n = FUSED ? (isk ? g.Kn : g.Vn) + (size_t)bh * S_new * DP : src_c;
+  const pk_u32x4 rs_c = rsrc_words(src_c, (uint32_t)((size_t)g.kv_rows * DP * 2));
+  const pk_u32x4 rs_n = rsrc_words(src_n, FUSED ? (uint32_t)((size_t)S_new * DP * 2) : 0u);
+  uint32_t voff0[NPW];
+  int lrow[NPW];
+#pragma unroll
+  for (int j = 0; j < NPW; ++j) {
+    const int qq = wq * NPW + j;
+    const int row = qq * RPI + lane / CH, sl = lane % CH;
+    const int lc = isk ? swz_k<CH>(sl, row) : (sl ^ swz_v<DP>(row));
+    lrow[j] = row;
+    voff0[j] = (uint32_t)(row * DP * 2 + 16 * lc);
+  }
+  auto issue = [&](int step, int stage) __attribute__((always_inline)) {
+    const int k0 = (t_begin + step) * BKV;
+    const bool nw = FUSED && k0 >= S_cache;
+    const pk_u32x4 rs = nw ? rs_n : rs_c;
+    const int r0 = nw ? k0 - S_cache : k0;  // first row of the step in its source
+    uint8_t *tile = ring + stage * 2 * TB + (isk ? 0 : TB);
+    if (k0 + BKV <= kv_end) {
+#pragma unroll
+      for (int j = 0; j < NPW; ++j)
+        dma_lds16(rs, tile + (wq * NPW + j) * 1024, voff0[j], (uint32_t)(r0 * DP * 2));
+    } else {
+#pragma unroll
+      for (int j = 0; j < NPW; ++j) {
+        const int over = max(0, k0 + lrow[j] - (kv_end - 1));  // rows past the last visible one
+        dma_lds16(rs, tile + (wq * NPW + j) * 1024, voff0[j] - (uint32_t)(over * DP * 2),
+                  (uint32_t)(r0 * DP * 2));
+      }
+    }
+  };
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_o[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const int q_limit = causal ? (off + my_q) : (g.S_kv - 1);
+  const float c2 = scale * 1.4426950408889634f;  // scale * log2(e)
+
+  // ---- one wave's block of a step: keys [kb0, kb0+32) x its 32 queries
+  auto kb0_of = [&](int step) __attribute__((always_inline)) { return (t_begin + step) * BKV + 32 * kh; };
+  // keys of the block visible to at least one of the wave's queries?
+  auto visible = [&](int step) __attribute__((always_inline)) {
+    const int kb0 = kb0_of(step);
+    return kb0 < kv_end && !(causal && kb0 > off + qw + 31);
+  };
+  // does any key of the block need masking for some query of the wave?
+  auto masked = [&](int step) __attribute__((always_inline)) {
+    const int kb0 = kb0_of(step);
+    return kb0 + 31 >= kv_end || (causal && kb0 + 31 > off + qw);
+  };
+  // S^T block = K Q^T (raw scores, unscaled)
+  auto qk = [&](int stage) __attribute__((always_inline)) -> f32x16 {
+    const uint8_t *ks = ring + stage * 2 * TB;
+    f32x16 sc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = 0.f;
+    const int row = 32 * kh + (lane & 31);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const u32x4 kv = *reinterpret_cast<const u32x4 *>(ks + row * DP * 2 + 16 * swz_k<CH>(2 * ds + h, row));
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kv), qf[ds], sc, 0, 0, 0);
+    }
+    return sc;
+  };
+  // Softmax in the log2 domain on unscaled scores: p = 2^(s c - m c) with
+  // c = scale * log2(e) (one FMA and v_exp_f32 per score).  The running max m
+  // used in the exponent is raised only when a new score exceeds it by more
+  // than 8 / c (p may reach 2^8 meanwhile); o = sum p v / sum p does not
+  // depend on it, and skipping most rescales saves the multiply of the whole
+  // accumulator.  Then O^T += V^T (P_hi + P_lo)^T.  MASKED is a compile-time
+  // flag so blocks off the diagonal carry no mask arithmetic.
+  auto softmax_pv = [&](auto mask_c, int step, int stage, f32x16 sc) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(mask_c)::value;
+    const uint8_t *vs = ring + stage * 2 * TB + TB;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if constexpr (MASKED) {
+        const int key = kb0_of(step) + (i >> 2) * 8 + h * 4 + (i & 3);
+        if (key > q_limit || key >= kv_end) sc[i] = -INFINITY;
+      }
+      tmax = fmaxf(tmax, sc[i]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    if (__any((tmax - m_run) * c2 > 8.0f)) {  // also true for the first block (m_run = -inf)
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run - m_new) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[db][e] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
+    float psum = 0.f;
+    uint32_t phi[8], plo[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], c2, -mc));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i + 1], c2, -mc));
+      psum += p0 + p1;
+      const uint32_t hh = pack_bf(p0, p1);
+      phi[i >> 1] = hh;
+      plo[i >> 1] = pack_bf(p0 - lo_bf(hh), p1 - hi_bf(hh));
+    }
+    psum += __shfl_xor(psum, 32, 64);
+    l_run += psum;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const u32x4 hv4 = {phi[4 * st + 0], phi[4 * st + 1], phi[4 * st + 2], phi[4 * st + 3]};
+      const u32x4 lv4 = {plo[4 * st + 0], plo[4 * st + 1], plo[4 * st + 2], plo[4 * st + 3]};
+      const bf16x8 pb_hi = __builtin_bit_cast(bf16x8, hv4);
+      const bf16x8 pb_lo = __builtin_bit_cast(bf16x8, lv4);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        i16x4 hv[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int key = 32 * kh + st * 16 + 8 * r + 4 * h + (gi >> 2);
+          const int d = db * 32 + 16 * (grp & 1) + 4 * (gi & 3);
+          const int c = d >> 3;
+          hv[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4 *)(vs + key * DP * 2 + 16 * (c ^ swz_v<DP>(key)) + 2 * (d & 7)));
+        }
+        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(hv[0], hv[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb_hi, acc_o[db], 0, 0, 0);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb_lo, acc_o[db], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- pipeline: step s waits for its own loads, one barrier, then the
+  // stage of step s-1 (free: every wave is past it) is refilled with step
+  // s+STAGES-1 and step s is computed.
+  using MaskT = std::integral_constant<bool, true>;
+  using NoMaskT = std::integral_constant<bool, false>;
+#pragma unroll
+  for (int p = 0; p < STAGES - 1; ++p)
+    if (p < nsteps) issue(p, p);
+  for (int s = 0; s < nsteps; ++s) {
+    if (s + STAGES - 2 < nsteps) vm_wait<(STAGES - 2) * NPW>();
+    else vm_wait<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // no LDS access moves above the barrier
+    if (s + STAGES - 1 < nsteps) issue(s + STAGES - 1, (s + STAGES - 1) % STAGES);
+    if (visible(s)) {
+      const f32x16 sc = qk(s % STAGES);
+      if (masked(s)) softmax_pv(MaskT{}, s, s % STAGES, sc);
+      else softmax_pv(NoMaskT{}, s, s % STAGES, sc);
+    }
+  }
+  vm_wait<0>();
+  __syncthreads();  // every wave is done with the ring
+
+  // ---- merge the KH partial states of each query in kh order
+  float *part = reinterpret_cast<float *>(ring) + wid * 32 * PS;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      part[(lane & 31) * PS + db * 32 + (i >> 2) * 8 + h * 4 + (i & 3)] = acc_o[db][i];
+  if (h == 0) {
+    ml_s[wid][lane & 31][0] = m_run;
+    ml_s[wid][lane & 31][1] = l_run;
+  }
+  __syncthreads();
+  constexpr int TPQ = FA_THREADS / BQ;  // threads per query
+  constexpr int DPT = DP / TPQ;         // outputs per thread
+  static_assert(DPT % 8 == 0, "16-byte stores");
+  const int ql = tid / TPQ, seg = tid % TPQ;
+  const int g2 = ql >> 5, qi = ql & 31;
+  const int q = q0 + ql;
+  if (q >= g.S_q) return;
+  // states are (m, l, o) with o, l relative to 2^(m c): weights 2^((m_k - M) c)
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < KH; ++k) M = fmaxf(M, ml_s[g2 + QG * k][qi][0]);
+  float wk[KH], L = 0.f;
+#pragma unroll
+  for (int k = 0; k < KH; ++k) {
+    const float mk = ml_s[g2 + QG * k][qi][0];
+    wk[k] = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mk - M) * c2);
+    L += ml_s[g2 + QG * k][qi][1] * wk[k];
+  }
+  const size_t orow = (size_t)bh * g.S_q + q;
+  if (g.splits == 1) {
+    const float inv = 1.0f / L;
+    uint32_t o[DPT / 2];
+#pragma unroll
+    for (int e = 0; e < DPT; e += 2) {
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < KH; ++k) {
+        const float *pk = reinterpret_cast<const float *>(ring) + (g2 + QG * k) * 32 * PS + qi * PS + seg * DPT + e;
+        a0 += pk[0] * wk[k];
+        a1 += pk[1] * wk[k];
+      }
+      o[e >> 1] = pack_bf(a0 * inv, a1 * inv);
+    }
+    uint16_t *op = g.O + orow * DP + seg * DPT;
+#pragma unroll
+    for (int e = 0; e < DPT / 8; ++e)
+      *reinterpret_cast<u32x4 *>(op + 8 * e) = u32x4{o[4 * e], o[4 * e + 1], o[4 * e + 2], o[4 * e + 3]};
+  } else {
+    // this split's state for the query: max Mu, sum L, unnormalised o
+    const size_t prow = (size_t)split * g.BH * g.S_q + orow;
+    float *po = g.part_o + prow * DP + seg * DPT;
+#pragma unroll
+    for (int e = 0; e < DPT; e += 4) {
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < KH; ++k) {
+        const float *pk = reinterpret_cast<const float *>(ring) + (g2 + QG * k) * 32 * PS + qi * PS + seg * DPT + e;
+        v += *reinterpret_cast<const f32x4 *>(pk) * wk[k];
+      }
+      *reinterpret_cast<f32x4 *>(po + e) = v;
+    }
+    if (seg == 0) {
+      g.part_ml[prow * 2] = M;
+      g.part_ml[prow * 2 + 1] = L;
+    }
+  }
+}
+
+// Merge of the key splits (split order), 8 outputs per thread with 16-byte
+// accesses: O = sum_s o_s w_s / sum_s l_s w_s, w_s = 2^((m_s - M) c) with m
+// the running max of unscaled scores and c = scale * log2(e).
+template <int DP>
+__global__ __launch_bounds__(256) void fa_combine_kernel(FaArgs g) {
+  const int64_t rows = (int64_t)g.BH * g.S_q;
+  const int64_t items = rows * (DP / 8);
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < items; t += (int64_t)gridDim.x * 256) {
+    const int64_t row = t / (DP / 8);
+    const int d0 = (int)(t % (DP / 8)) * 8;
+    const float c2 = g.scale * 1.4426950408889634f;
+    float M = -INFINITY;
+    for (int s = 0; s < g.splits; ++s) M = fmaxf(M, g.part_ml[((size_t)s * rows + row) * 2]);
+    float L = 0.f;
+    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+    for (int s = 0; s < g.splits; ++s) {
+      const size_t pr = (size_t)s * rows + row;
+      const float ms = g.part_ml[pr * 2];
+      const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ms - M) * c2);
+      L += g.part_ml[pr * 2 + 1] * w;
+      a0 += *reinterpret_cast<const f32x4 *>(g.part_o + pr * DP + d0) * w;
+      a1 += *reinterpret_cast<const f32x4 *>(g.part_o + pr * DP + d0 + 4) * w;
+    }
+    const float inv = 1.0f / L;
+    const u32x4 o = {pack_bf(a0[0] * inv, a0[1] * inv), pack_bf(a0[2] * inv, a0[3] * inv),
+                     pack_bf(a1[0] * inv, a1[1] * inv), pack_bf(a1[2] * inv, a1[3] * inv)};
+    *reinterpret_cast<u32x4 *>(g.O + row * DP + d0) = o;
+  }
+}
+
 int pick_splits(int BH, int q_tiles, int kv_tiles) {
   int s = 1;
   while (BH * q_tiles * s < 256 && kv_tiles / (2 * s) >= 4) s *= 2;
@@ -368,8 +744,70 @@ int attention_dp(AttArgs g, hipStream_t st) {
 int kv_append_inplace_launch(uint16_t *cache, const uint16_t *neu, int64_t BH, int64_t Sc,
                              int64_t Sn, int64_t D, int64_t cap, hipStream_t st);
 
+// The flash-style kernel when the shape suits it: D 64 or 128 and 16-byte
+// aligned tensors (callers also require scale > 0: the kernel tracks the
+// running max on unscaled scores).  With Kn/Vn (fused append) the new rows must start on a
+// 64-key step (S_cache a multiple of 64).
+bool fa_applicable(int S_kv, int S_cache, int D, int kv_rows, const void *Q, const void *K, const void *V,
+                   const void *O, const void *Kn, const void *Vn, const void *Kc, const void *Vc) {
+  if (D != 64 && D != 128) return false;
+  if (S_kv <= 0) return false;
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return false;
+  if ((size_t)kv_rows * D * 2 >= (size_t(1) << 31)) return false;
+  if (Kn) {
+    if (!aligned16(Kn) || !aligned16(Vn) || !aligned16(Kc) || !aligned16(Vc)) return false;
+    if (S_cache % 64 != 0) return false;  // one source per 64-key step
+    if ((size_t)(S_kv - S_cache) * D * 2 >= (size_t(1) << 31)) return false;
+  }
+  return true;
+}
+
+// Launch the flash-style kernel: 128 queries per workgroup (4 query groups x
+// 2 key halves of a 64-key step) and enough key splits to reach ~256
+// workgroups, each split keeping >= 8 steps.
+int attention_fa(FaArgs a, int D, hipStream_t st) {
+  constexpr int QG = 4, BQ = 128, BKV = 64;
+  a.q_tiles = (a.S_q + BQ - 1) / BQ;
+  const int ntiles = (a.S_kv + BKV - 1) / BKV;
+  a.splits = 1;
+  while ((int64_t)a.BH * a.q_tiles * a.splits < 256 && ntiles / (2 * a.splits) >= 8 && a.splits < 8) a.splits *= 2;
+  if (a.splits > 1) {
+    const size_t rows = (size_t)a.BH * a.S_q;
+    const size_t bytes_o = (size_t)a.splits * rows * D * sizeof(float);
+    const size_t bytes = bytes_o + (size_t)a.splits * rows * 2 * sizeof(float);
+    void *ws = nullptr;
+    int rc = library_workspace(bytes, &ws);
+    if (rc) return rc;
+    a.part_o = static_cast<float *>(ws);
+    a.part_ml = reinterpret_cast<float *>(static_cast<char *>(ws) + bytes_o);
+  }
+  const int blocks = a.BH * a.q_tiles * a.splits;
+  const bool fused = a.Kn != nullptr;
+  if (D == 128) {
+    if (fused) attention_fa_kernel<128, QG, true><<<blocks, FA_THREADS, 0, st>>>(a);
+    else attention_fa_kernel<128, QG, false><<<blocks, FA_THREADS, 0, st>>>(a);
+  } else {
+    if (fused) attention_fa_kernel<64, QG, true><<<blocks, FA_THREADS, 0, st>>>(a);
+    else attention_fa_kernel<64, QG, false><<<blocks, FA_THREADS, 0, st>>>(a);
+  }
+  PK_LAUNCH_CHECK("attention_fa_kernel");
+  if (a.splits > 1) {
+    const int64_t items = (int64_t)a.BH * a.S_q * (D / 8);
+    const int grid = (int)std::min<int64_t>((items + 255) / 256, 8192);
+    if (D == 128) fa_combine_kernel<128><<<grid, 256, 0, st>>>(a);
+    else fa_combine_kernel<64><<<grid, 256, 0, st>>>(a);
+    PK_LAUNCH_CHECK("fa_combine_kernel");
+  }
+  return PK_OK;
+}
+
 int attention_run(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O, int BH,
                   int S_q, int S_kv, int D, int kv_rows, float scale, int causal, hipStream_t st) {
+  if (scale > 0.f && fa_applicable(S_kv, S_kv, D, kv_rows, Q, K, V, O, nullptr, nullptr, nullptr, nullptr)) {
+    FaArgs a{Q, K, V, nullptr, nullptr, nullptr, nullptr, O, nullptr, nullptr, BH, S_q, S_kv, S_kv, kv_rows,
+             scale, causal, 1, 1};
+    return attention_fa(a, D, st);
+  }
   AttArgs g{Q, K, V, O, nullptr, nullptr, BH, S_q, S_kv, D, kv_rows, scale, causal, 1, 1};
   if (D <= 32) return attention_dp<32>(g, st);
   if (D <= 64) return attention_dp<64>(g, st);
@@ -408,6 +846,14 @@ int launch_fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *
   hipStream_t st = (hipStream_t)stream;
   const int64_t BH = (int64_t)B * H;
   if (BH == 0) return PK_OK;
+  const int S_kv = S_cache + S_q;
+  if (S_q > 0 && BH <= INT32_MAX && scale > 0.f &&
+      fa_applicable(S_kv, S_cache, D, cache_capacity, Q, Kc, Vc, O, Kn, Vn, Kc, Vc)) {
+    // the append happens inside the attention kernel
+    FaArgs a{Q, Kc, Vc, Kn, Vn, Kc, Vc, O, nullptr, nullptr, (int)BH, S_q, S_kv, S_cache, cache_capacity,
+             scale, causal, 1, 1};
+    return attention_fa(a, D, st);
+  }
   int rc = kv_append_inplace_launch(Kc, Kn, BH, S_cache, S_q, D, cache_capacity, st);
   if (rc) return rc;
   rc = kv_append_inplace_launch(Vc, Vn, BH, S_cache, S_q, D, cache_capacity, st);

@@ -154,13 +154,17 @@ __device__ __forceinline__ pk_u32x4 rsrc_words(const void *base, uint32_t bytes)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_lds16(pk_u32x4 rsrc, const void *lds, uint32_t voff, uint32_t soff) {
-  // lds and soff are wave-uniform; readfirstlane keeps them in SGPRs (the
-  // "s" constraint does not move a VGPR value by itself)
+  // lds, soff and rsrc are wave-uniform; readfirstlane keeps them in SGPRs
+  // (the "s" constraint does not move a VGPR value by itself)
   const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)reinterpret_cast<uintptr_t>((lds_void *)lds));
   const int so = __builtin_amdgcn_readfirstlane((int)soff);
+  const pk_u32x4 rs = {(uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[0]),
+                       (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[1]),
+                       (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[2]),
+                       (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[3])};
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
+               : "s"(m0), "v"(voff), "s"(rs), "s"(so)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop

@@ -428,6 +428,54 @@ def test_attention_prefill(gpu, oracle, B, H, Sq, Skv, D, causal):
     assert _att_bound_bad(oracle, got, want, q, k, v, causal) == 0, rep
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 64, 128, 128, 64), (2, 32, 130, 400, 128),
+                                          (1, 128, 64, 64, 128), (1, 128, 200, 1000, 64),
+                                          (1, 4, 64, 4096, 64), (1, 2, 200, 2100, 128)])
+def test_attention_prefill_flash_path(gpu, oracle, B, H, Sq, Skv, D, causal):
+    """Head dims 64 and 128 take the flash-style kernel: ragged query and key
+    counts (not multiples of 128 / 64), and small grids whose key range is
+    split over up to 8 workgroups and merged by the combine kernel."""
+    _say(f"attention flash {B},{H},{Sq},{Skv},{D} causal={causal}")
+    q, k, v = rng_bf16((B, H, Sq, D), 90), rng_bf16((B, H, Skv, D), 91), rng_bf16((B, H, Skv, D), 92)
+    got = from_dev(K().attention_prefill(to_dev(q), to_dev(k), to_dev(v), None, causal))
+    want = oracle.attention_prefill(q, k, v, None, causal)
+    rep = mt.report(got, want)
+    _say(f"attention flash: {rep}")
+    assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+    assert _att_bound_bad(oracle, got, want, q, k, v, causal) == 0, rep
+
+
+@pytest.mark.parametrize("Sc,D", [(192, 128), (201, 128), (128, 64), (130, 64)])
+def test_fused_kv_append_attention_flash_path(gpu, oracle, Sc, D):
+    """In-place append fused into the flash kernel (S_cache a multiple of its
+    64-key step) and the fallback (separate append kernels) otherwise; the
+    cache is checked bit-exactly, including the rows past S_cache + S_q that
+    must stay untouched."""
+    import torch
+
+    B, H, Sq = 2, 32, 70
+    _say(f"fused append flash Sc={Sc} D={D}")
+    q = rng_bf16((B, H, Sq, D), 93)
+    kn, vn = rng_bf16((B, H, Sq, D), 94), rng_bf16((B, H, Sq, D), 95)
+    kc, vc = rng_bf16((B, H, Sc, D), 96), rng_bf16((B, H, Sc, D), 97)
+    cap = Sc + Sq + 5
+    kcd = torch.full((B, H, cap, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    vcd = torch.full_like(kcd, -3.0)
+    kcd[:, :, :Sc] = to_dev(kc)
+    vcd[:, :, :Sc] = to_dev(vc)
+    got = from_dev(K().fused_kv_append_attention(to_dev(q), to_dev(kn), to_dev(vn), kcd, vcd, Sc))
+    kfull, vfull = oracle.kv_append(kc, kn), oracle.kv_append(vc, vn)
+    kd, vd = from_dev(kcd), from_dev(vcd)
+    assert np.array_equal(kd[:, :, :Sc + Sq], kfull) and np.array_equal(vd[:, :, :Sc + Sq], vfull)
+    assert np.all(kd[:, :, Sc + Sq:] == bf([7.0])[0]) and np.all(vd[:, :, Sc + Sq:] == bf([-3.0])[0])
+    want = oracle.attention_prefill(q, kfull, vfull, None, True)
+    rep = mt.report(got, want)
+    _say(f"fused append flash: {rep}")
+    assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+    assert _att_bound_bad(oracle, got, want, q, kfull, vfull, True) == 0, rep
+
+
 def test_attention_leaky_mask_is_detected(gpu, oracle):
     q, k, v = rng_bf16((1, 2, 64, 64), 73), rng_bf16((1, 2, 64, 64), 74), rng_bf16((1, 2, 64, 64), 75)
     leak = from_dev(K().attention_prefill(to_dev(q), to_dev(k), to_dev(v), None, False))
