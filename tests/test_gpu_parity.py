@@ -185,6 +185,19 @@ def test_matmul_random(gpu, oracle, M, N, Kd):
     assert _err_bound_ok(got, want, _abs_dot(a, b), Kd) == 0, rep
 
 
+@pytest.mark.parametrize("M,N,Kd", [(130, 200, 832), (33, 72, 128), (64, 3072, 768)])
+def test_fused_rmsnorm_matmul_gamma_shapes(gpu, oracle, M, N, Kd):
+    x = synth.normal_bf16((M, Kd), 26)
+    g = synth.normal_bf16((Kd,), 27, 0.1, 1.0)
+    w = synth.normal_bf16((Kd, N), 28, 1.0 / np.sqrt(Kd))
+    got = from_dev(K().fused_rmsnorm_matmul(to_dev(x), to_dev(w), to_dev(g), 1e-6))
+    want = oracle.fused_rmsnorm_matmul(x, w, g, 1e-6)
+    rep = mt.report(got, want)
+    assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.98, rep
+    a = oracle.rmsnorm(x, g, 1e-6)
+    assert _err_bound_ok(got, want, _abs_dot(a, w), Kd, operand_ulps=1.0) == 0, rep
+
+
 def test_fused_rmsnorm_matmul_config1(gpu, oracle):
     """Config 1: x [128,768] N(0,1), gamma 1+0.1N, eps 1e-6, W [768,3072] N(0,1/768)."""
     x = synth.normal_bf16((128, 768), 21)
@@ -199,8 +212,11 @@ def test_fused_rmsnorm_matmul_config1(gpu, oracle):
     assert _err_bound_ok(got, want, _abs_dot(a, w), 768, operand_ulps=1.0) == 0, rep
 
 
-@pytest.mark.parametrize("M,N,Kd", [(64, 128, 64), (130, 200, 1600), (40, 96, 2048)])
+@pytest.mark.parametrize("M,N,Kd", [(64, 128, 64), (130, 200, 1600), (40, 96, 2048), (130, 200, 832),
+                                    (33, 72, 128), (40, 96, 1024)])
 def test_fused_rmsnorm_matmul_no_gamma(gpu, oracle, M, N, Kd):
+    """K <= 832: the latency-oriented kernel (ragged M and N); K <= 1536: the
+    panel kernel; longer rows: RMSNorm into workspace, then the GEMM."""
     x = synth.normal_bf16((M, Kd), 24)
     w = synth.normal_bf16((Kd, N), 25, 1.0 / np.sqrt(Kd))
     got = from_dev(K().fused_rmsnorm_matmul(to_dev(x), to_dev(w), None, 1e-5))
