@@ -176,23 +176,45 @@ PK_API int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C
  * 5 uses all 160 KiB of LDS).  Process-wide; default 5. */
 PK_API int pk_gemm_set_ring_depth(int depth);
 
-/* Launch configuration of the streaming int8 kernel (the fast path of
- * launch_matmul_int8 when N % 16 == 0, K % 64 == 0 and A, Wq, scale, C are
- * 16-byte aligned).  Field names follow the tuning-cache config
- * (tuning/schema.json:65-79): block_n = output columns per workgroup, split
- * over num_warps waves of 16..256 columns each (see the variant table in
- * int8.hip); block_k = rows of K one workgroup reduces (a multiple of 64;
- * K / block_k workgroups per column slice, their fp32 partials summed by a
- * second kernel); shared_memory_stages = per-wave LDS ring depth in 64-row
- * steps; block_m = rows of A per workgroup (16, 32 or 64).  0 in any field
- * selects the built-in choice for it. */
-typedef struct pk_int8_config {
-  int block_m, block_n, block_k, num_warps, shared_memory_stages;
-} pk_int8_config;
+/* ---- configurations (tuning-cache vocabulary) ------------------------------ */
+
+/* One kernel configuration; the fields are those of the tuning-cache schema
+ * (tuning/schema.json:65-79).  num_warps counts 64-lane waves.  In a request
+ * a 0 field means "any".  Meaning per op family:
+ *   GEMM (matmul, fused_matmul_bias_gelu, fused_matmul_bias_residual):
+ *     block_m x block_n output tile, block_k = k-tile per LDS stage,
+ *     shared_memory_stages = LDS ring depth, vector_width = bf16 per global
+ *     load (8, or 1 on the unaligned path), unroll = 32x32x16 MFMA k-steps
+ *     per stage.  Variants: 256x256x32 DMA ring of 4 or 5 stages (4 waves),
+ *     256x256x64 register-staged (8 waves), 128x128x64 and 64x64x64 (4 waves).
+ *   int8 (matmul_int8, matmul_int8_gelu, matmul_int8_residual): block_n =
+ *     output columns per workgroup, split over num_warps waves of 16..256
+ *     columns each; block_k = rows of K one workgroup reduces (a multiple of
+ *     64; K / block_k workgroups per column slice, fp32 partials summed by a
+ *     second kernel); shared_memory_stages = per-wave ring depth in 64-row
+ *     steps; block_m = rows of A per workgroup (16, 32 or 64); vector_width
+ *     = 16 (int8 per DMA lane); unroll = 2 (16x16x32 MFMA k-steps per step).
+ *   fused_rmsnorm_matmul, fused_residual_rmsnorm, fused_softmax_mask,
+ *     fused_kv_append_attention: one fixed configuration per shape that
+ *     describes the kernel the entry point runs (see pk_op_configs). */
+typedef struct pk_config {
+  int block_m, block_n, block_k, num_warps, vector_width, unroll, shared_memory_stages;
+} pk_config;
+
+/* Every configuration the kernels implement for `op` at shape (M, N, K) --
+ * the shape key of the op as the runtime defines it (GEMM-like ops: M, N, K;
+ * row-wise ops: rows, cols, 0; fused_kv_append_attention: S_q, S_kv, D).
+ * Writes min(total, cap) configurations to `out` (may be NULL when cap is 0)
+ * and returns the total (0 for a shape no variant takes), or
+ * PK_ERR_INVALID_ARG for an unknown op.  No device is needed. */
+PK_API int pk_op_configs(const char *op, long long M, long long N, long long K, pk_config *out, int cap);
+/* The configuration the op's plain entry point chooses for 16-byte aligned
+ * operands (PK_ERR_UNSUPPORTED when it takes a generic fallback kernel). */
+PK_API int pk_op_default_config(const char *op, long long M, long long N, long long K, pk_config *out);
 
 /* The configuration launch_matmul_int8 would use for this shape (returns
  * PK_ERR_UNSUPPORTED when the shape takes the generic kernel). */
-PK_API int pk_int8_default_config(int M, int N, int K, pk_int8_config *out);
+PK_API int pk_int8_default_config(int M, int N, int K, pk_config *out);
 
 /* Tuning/test hook: int8 matmul with an explicit epilogue (0 none, 1 GELU,
  * 2 residual add of R [M,N]) and configuration (NULL = built-in choice).
@@ -200,8 +222,41 @@ PK_API int pk_int8_default_config(int M, int N, int K, pk_int8_config *out);
  * NULL: library-owned) holds the split partials. */
 PK_API int pk_matmul_int8_ex(int epi, const uint16_t *A, const int8_t *Wq, const float *scale,
                              uint16_t *C, const uint16_t *R, int M, int N, int K,
-                             const pk_int8_config *cfg, void *workspace, size_t workspace_bytes,
+                             const pk_config *cfg, void *workspace, size_t workspace_bytes,
                              void *stream);
+
+/* GEMM with an explicit epilogue (as pk_gemm_ex) and configuration (NULL =
+ * built-in choice).  A configuration no variant matches, or one that needs
+ * 16-byte aligned operands they do not have, returns PK_ERR_UNSUPPORTED. */
+PK_API int pk_gemm_config_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C,
+                             const uint16_t *bias, const uint16_t *R, int M, int N, int K,
+                             const pk_config *cfg, void *stream);
+
+/* ---- naive device goldens (the autotuner's correctness gate) --------------- */
+/* Straightforward one-thread-per-output kernels that restate the reference
+ * semantics in their own sequential order (fp32 multiply then add, no
+ * contraction; per-stage bf16 rounding; GELU with a double-precision erf).
+ * Slow by design; asynchronous on `stream`. */
+/* epi as pk_gemm_ex (0 none, 1 bias+GELU, 2 bias+residual, 3 residual). */
+PK_API int pk_naive_matmul(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
+                           const uint16_t *R, int M, int N, int K, void *stream);
+/* epi as pk_matmul_int8_ex (0 none, 1 GELU, 2 residual). */
+PK_API int pk_naive_matmul_int8(int epi, const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C,
+                                const uint16_t *R, int M, int N, int K, void *stream);
+/* out = rmsnorm(r ? bf16(x + r) : x, gamma, eps); r and gamma may be NULL. */
+PK_API int pk_naive_rmsnorm(const uint16_t *x, const uint16_t *r, const uint16_t *gamma, uint16_t *out,
+                            int rows, int cols, float eps, void *stream);
+/* out = softmax(bf16(bf16(logits) + mask)). */
+PK_API int pk_naive_softmax_mask(const float *logits, const uint16_t *mask, uint16_t *out, int rows, int cols,
+                                 void *stream);
+/* O [BH,S_q,D] over K/V rows [BH, kv_stride rows, D] (the first S_kv used). */
+PK_API int pk_naive_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O, int BH,
+                              int S_q, int S_kv, int kv_stride, int D, float scale, int causal, void *stream);
+/* Parity metrics of got vs want (bf16, n elements) in float64: out[0] cosine,
+ * out[1] max_rel_err (eps 1e-6), out[2] pcc, out[3] bit-exact fraction.
+ * Definitions of tests/golden/metrics.py:20-77.  Synchronous on `stream`;
+ * allocates a small device buffer. */
+PK_API int pk_compare_bf16(const uint16_t *got, const uint16_t *want, long long n, double out[4], void *stream);
 
 /* ---- synthetic inputs (host, deterministic, OpenMP) -------------------- */
 

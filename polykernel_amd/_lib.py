@@ -1,4 +1,5 @@
-"""ctypes binding of libpolykernel_amd.so (the C-ABI of include/polykernel_amd.h).
+"""ctypes binding of libpolykernel_amd.so (the C-ABI of include/polykernel_amd.h
+and include/polykernel_amd_runtime.h).
 
 The library is loaded from the package directory only.  If it is missing the
 import fails loudly -- there is no CPU fallback for any kernel.
@@ -19,6 +20,7 @@ PK_ERR_WORKSPACE = -3
 PK_ERR_NO_DEVICE = -4
 PK_ERR_UNSUPPORTED = -5
 PK_ERR_HIP = -6
+PK_ERR_NOT_FOUND = -7
 
 
 class PolyKernelError(RuntimeError):
@@ -30,11 +32,13 @@ class PolyKernelError(RuntimeError):
         self.message = message
 
 
-class Int8Config(C.Structure):
-    """struct pk_int8_config (include/polykernel_amd.h); 0 = built-in choice."""
+class Config(C.Structure):
+    """struct pk_config (include/polykernel_amd.h): one kernel configuration in
+    the tuning-cache vocabulary; 0 in a request means "any"."""
 
     _fields_ = [("block_m", C.c_int), ("block_n", C.c_int), ("block_k", C.c_int),
-                ("num_warps", C.c_int), ("shared_memory_stages", C.c_int)]
+                ("num_warps", C.c_int), ("vector_width", C.c_int), ("unroll", C.c_int),
+                ("shared_memory_stages", C.c_int)]
 
     def as_dict(self) -> dict:
         return {f: getattr(self, f) for f, _ in self._fields_}
@@ -47,6 +51,7 @@ SZ = C.c_size_t
 U64 = C.c_uint64
 I64 = C.c_int64
 D = C.c_double
+LL = C.c_longlong
 
 # name -> (restype, argtypes); mirrors include/polykernel_amd.h
 SIGNATURES = {
@@ -77,8 +82,42 @@ SIGNATURES = {
     "launch_decode_mlp_int8": (I, [P, P, P, P, P, P, I, I, I, P, SZ, P]),
     "pk_gemm_ex": (I, [I, P, P, P, P, P, I, I, I, I, P]),
     "pk_gemm_set_ring_depth": (I, [I]),
-    "pk_int8_default_config": (I, [I, I, I, C.POINTER(Int8Config)]),
-    "pk_matmul_int8_ex": (I, [I, P, P, P, P, P, I, I, I, C.POINTER(Int8Config), P, SZ, P]),
+    "pk_int8_default_config": (I, [I, I, I, C.POINTER(Config)]),
+    "pk_matmul_int8_ex": (I, [I, P, P, P, P, P, I, I, I, C.POINTER(Config), P, SZ, P]),
+    "pk_gemm_config_ex": (I, [I, P, P, P, P, P, I, I, I, C.POINTER(Config), P]),
+    "pk_op_configs": (I, [C.c_char_p, LL, LL, LL, C.POINTER(Config), I]),
+    "pk_op_default_config": (I, [C.c_char_p, LL, LL, LL, C.POINTER(Config)]),
+    "pk_naive_matmul": (I, [I, P, P, P, P, P, I, I, I, P]),
+    "pk_naive_matmul_int8": (I, [I, P, P, P, P, P, I, I, I, P]),
+    "pk_naive_rmsnorm": (I, [P, P, P, P, I, I, F, P]),
+    "pk_naive_softmax_mask": (I, [P, P, P, I, I, P]),
+    "pk_naive_attention": (I, [P, P, P, P, I, I, I, I, I, F, I, P]),
+    "pk_compare_bf16": (I, [P, P, LL, C.POINTER(D), P]),
+    # runtime layer (include/polykernel_amd_runtime.h)
+    "pk_last_text": (C.c_char_p, []),
+    "pk_cache_create": (P, []),
+    "pk_cache_destroy": (None, [P]),
+    "pk_cache_load_tuning": (I, [P, C.c_char_p]),
+    "pk_cache_put": (I, [P, C.c_char_p]),
+    "pk_cache_size": (LL, [P]),
+    "pk_cache_serialize": (I, [P]),
+    "pk_cache_select": (I, [P, C.c_char_p, C.c_char_p, LL, LL, LL, C.c_char_p]),
+    "pk_cache_put_binary": (I, [P, C.c_char_p, C.c_char_p, LL, LL, LL, C.c_char_p, C.c_char_p, C.c_char_p]),
+    "pk_cache_get_binary": (I, [P, C.c_char_p, C.c_char_p, LL, LL, LL, C.c_char_p]),
+    "pk_cache_persist": (I, [P, C.c_char_p]),
+    "pk_cache_load_persisted": (I, [P, C.c_char_p]),
+    "pk_cache_invalidate_stale": (LL, [P]),
+    "pk_hash_file": (I, [C.c_char_p]),
+    "pk_format_key": (I, [C.c_char_p, C.c_char_p, LL, LL, LL, C.c_char_p]),
+    "pk_passes_correctness_gate": (I, [D, D, D, D]),
+    "pk_rel_ceiling": (D, [C.c_char_p, LL]),
+    "pk_select_best_validated": (I, [C.POINTER(I), C.POINTER(D), I]),
+    "pk_config_candidates": (I, [C.c_char_p, LL, LL, LL, C.c_char_p]),
+    "pk_runtime_create": (P, [P, C.c_char_p]),
+    "pk_runtime_destroy": (None, [P]),
+    "pk_runtime_resolve": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p]),
+    "pk_runtime_run": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p, P]),
+    "pk_autotune": (I, [C.c_char_p, LL, LL, LL, C.c_char_p, C.c_char_p]),
     "pk_synth_normal_bf16": (None, [U64, U64, D, D, P, I64]),
     "pk_synth_normal_f32": (None, [U64, U64, D, D, P, I64]),
     "pk_synth_mask_bf16": (None, [U64, U64, D, P, I64]),
@@ -114,3 +153,9 @@ def last_error() -> str:
 def check(rc: int, name: str) -> None:
     if rc != PK_OK:
         raise PolyKernelError(name, rc, last_error())
+
+
+def last_text() -> str:
+    """Text result of the last runtime call that produced one (pk_last_text)."""
+    t = load().pk_last_text()
+    return t.decode() if t else ""

@@ -3,8 +3,11 @@
     python -m polykernel_amd.build          # -> polykernel_amd/libpolykernel_amd.so
 
 Every csrc/*.hip file is compiled by hipcc for gfx950 only (no CUDA, no other
-targets) and linked into one shared library whose exported symbols are the
-C-ABI of include/polykernel_amd.h.  Packed-fp32 instruction selection is turned
+targets), every csrc/runtime/*.cpp file (host-only: tuning cache, kernel cache,
+runtime, autotuner) by g++ as C++20, and both are linked into one shared
+library exporting the C-ABI of include/polykernel_amd.h and
+include/polykernel_amd_runtime.h plus the C++ API of
+include/polykernel_amd_runtime.hpp.  Packed-fp32 instruction selection is turned
 off (-packed-fp32-ops); fp32 division and square root keep HIP's correctly
 rounded defaults (no fast-math).
 """
@@ -40,20 +43,31 @@ COMMON_FLAGS = [
 ]
 
 
+# Host-only runtime (tuning cache, kernel cache, autotuner): plain C++20.
+CXX = shutil.which("g++") or "g++"
+HOST_FLAGS = [
+    "-std=c++20", "-O2", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra", "-Wno-unused-parameter",
+    "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-I", str(PKG.parent / "include"),
+]
+
+
 def _compile(src: Path) -> Path:
-    out = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(out)]
+    out = OBJ / (src.stem + (".o" if src.suffix == ".hip" else ".host.o"))
+    if src.suffix == ".cpp":
+        cmd = [CXX, *HOST_FLAGS, "-c", str(src), "-o", str(out)]
+    else:
+        cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         msg = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
-        raise RuntimeError(f"hipcc failed for {src.name}:\n{msg}")
+        raise RuntimeError(f"{Path(cmd[0]).name} failed for {src.name}:\n{msg}")
     return out
 
 
 def build(verbose: bool = True) -> Path:
     """Compile every kernel source and link libpolykernel_amd.so (always rebuilds)."""
     OBJ.mkdir(exist_ok=True)
-    srcs = sorted(CSRC.glob("*.hip"))
+    srcs = sorted(CSRC.glob("*.hip")) + sorted((CSRC / "runtime").glob("*.cpp"))
     if not srcs:
         raise RuntimeError(f"no sources under {CSRC}")
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)

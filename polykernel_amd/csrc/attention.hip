@@ -801,6 +801,21 @@ int attention_fa(FaArgs a, int D, hipStream_t st) {
   return PK_OK;
 }
 
+// The kernel attention runs for aligned operands and scale > 0, as a config:
+// the flash-style kernel for D 64 / 128 (128 queries x 64-key steps, 8 waves,
+// K/V ring of 128 KiB / (2 * 64 * D * 2) steps), the generic one otherwise.
+// unroll = MFMA k-steps of one query-key product.
+bool attention_config(int S_q, int S_kv, int D, pk_config *out) {
+  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 128) return false;
+  if (D == 64 || D == 128) {
+    *out = pk_config{128, 64, D, FA_WAVES, 8, D / 16, FA_RING / (2 * 64 * D * 2)};
+  } else {
+    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : 128;
+    *out = pk_config{AT_BQ, AT_BKV, dp, AT_WAVES, D % 8 == 0 ? 8 : 1, dp / 16, 1};
+  }
+  return true;
+}
+
 int attention_run(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O, int BH,
                   int S_q, int S_kv, int D, int kv_rows, float scale, int causal, hipStream_t st) {
   if (scale > 0.f && fa_applicable(S_kv, S_kv, D, kv_rows, Q, K, V, O, nullptr, nullptr, nullptr, nullptr)) {

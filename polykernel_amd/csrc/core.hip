@@ -196,25 +196,105 @@ int pk_check_bf16_conversion(unsigned long long *mismatches) {
   return PK_OK;
 }
 
+// The bare arch token of a gcnArchName: the first "gfx" followed by a digit,
+// through the run of lower-case letters and digits after it
+// ("gfx950:sramecc+:xnack-" -> "gfx950"); "" when there is none
+// (lib/Runtime/DeviceDetect.cpp:28-50 of the reference).
 int pk_parse_gcn_arch_name(const char *name, char *buf, int buf_len) {
   if (!name || !buf || buf_len <= 0) {
     set_error("pk_parse_gcn_arch_name: null argument");
     return PK_ERR_INVALID_ARG;
   }
   buf[0] = '\0';
-  // Leading "gfx" followed by hex-ish digits/letters up to ':' (e.g. gfx950, gfx90a).
-  if (std::strncmp(name, "gfx", 3) != 0) return PK_OK;
+  const char *p = std::strstr(name, "gfx");
+  if (!p || p[3] < '0' || p[3] > '9') return PK_OK;
   int n = 3;
-  while (name[n] && name[n] != ':' &&
-         ((name[n] >= '0' && name[n] <= '9') || (name[n] >= 'a' && name[n] <= 'f')))
-    ++n;
-  if (n == 3) return PK_OK;
+  while ((p[n] >= '0' && p[n] <= '9') || (p[n] >= 'a' && p[n] <= 'z')) ++n;
   if (n + 1 > buf_len) {
     set_error("pk_parse_gcn_arch_name: buffer too small");
     return PK_ERR_INVALID_ARG;
   }
-  std::memcpy(buf, name, n);
+  std::memcpy(buf, p, n);
   buf[n] = '\0';
+  return PK_OK;
+}
+
+// ---- configurations ---------------------------------------------------------
+
+namespace {
+enum OpFamily { OF_UNKNOWN, OF_GEMM, OF_INT8, OF_RMSNORM_MATMUL, OF_RMSNORM, OF_SOFTMAX, OF_ATTENTION };
+
+OpFamily op_family(const char *op) {
+  static const struct {
+    const char *name;
+    OpFamily family;
+  } kOps[] = {{"matmul", OF_GEMM},
+              {"fused_matmul_bias_gelu", OF_GEMM},
+              {"fused_matmul_bias_residual", OF_GEMM},
+              {"matmul_int8", OF_INT8},
+              {"matmul_int8_gelu", OF_INT8},
+              {"matmul_int8_residual", OF_INT8},
+              {"fused_rmsnorm_matmul", OF_RMSNORM_MATMUL},
+              {"fused_residual_rmsnorm", OF_RMSNORM},
+              {"fused_softmax_mask", OF_SOFTMAX},
+              {"fused_kv_append_attention", OF_ATTENTION}};
+  if (!op) return OF_UNKNOWN;
+  for (const auto &o : kOps)
+    if (std::strcmp(op, o.name) == 0) return o.family;
+  return OF_UNKNOWN;
+}
+
+bool dims_ok(long long M, long long N, long long K) {
+  return M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX;
+}
+
+// One fixed configuration (or none) as a list.
+int single(bool ok, const pk_config &c, pk_config *out, int cap) {
+  if (!ok) return 0;
+  if (out && cap > 0) out[0] = c;
+  return 1;
+}
+}  // namespace
+
+int pk_op_configs(const char *op, long long M, long long N, long long K, pk_config *out, int cap) {
+  const OpFamily f = op_family(op);
+  PK_CHECK_ARG(f != OF_UNKNOWN, "pk_op_configs: unknown op '%s'", op ? op : "(null)");
+  PK_CHECK_ARG(cap >= 0 && (out || cap == 0), "pk_op_configs: invalid output buffer");
+  if (!dims_ok(M, N, K)) return 0;
+  const int m = (int)M, n = (int)N, k = (int)K;
+  pk_config c{};
+  switch (f) {
+    case OF_GEMM: return gemm_configs(m, n, k, out, cap);
+    case OF_INT8: return int8_configs(m, n, k, out, cap);
+    case OF_RMSNORM_MATMUL: return single(rmsnorm_matmul_config(m, n, k, &c), c, out, cap);
+    case OF_RMSNORM: return single(k == 0 && rmsnorm_config(m, n, &c), c, out, cap);
+    case OF_SOFTMAX: return single(k == 0 && softmax_config(m, n, &c), c, out, cap);
+    case OF_ATTENTION: return single(n >= m && attention_config(m, n, k, &c), c, out, cap);
+    default: return 0;
+  }
+}
+
+int pk_op_default_config(const char *op, long long M, long long N, long long K, pk_config *out) {
+  const OpFamily f = op_family(op);
+  PK_CHECK_ARG(f != OF_UNKNOWN, "pk_op_default_config: unknown op '%s'", op ? op : "(null)");
+  PK_CHECK_ARG(out != nullptr, "pk_op_default_config: null output");
+  bool ok = false;
+  if (dims_ok(M, N, K)) {
+    const int m = (int)M, n = (int)N, k = (int)K;
+    switch (f) {
+      case OF_GEMM: ok = gemm_default(m, n, k, out); break;
+      case OF_INT8: ok = int8_default(m, n, k, out); break;
+      case OF_RMSNORM_MATMUL: ok = rmsnorm_matmul_config(m, n, k, out); break;
+      case OF_RMSNORM: ok = k == 0 && rmsnorm_config(m, n, out); break;
+      case OF_SOFTMAX: ok = k == 0 && softmax_config(m, n, out); break;
+      case OF_ATTENTION: ok = n >= m && attention_config(m, n, k, out); break;
+      default: break;
+    }
+  }
+  if (!ok) {
+    set_error("pk_op_default_config: %s has no configuration for M=%lld N=%lld K=%lld", op, M, N, K);
+    return PK_ERR_UNSUPPORTED;
+  }
   return PK_OK;
 }
 

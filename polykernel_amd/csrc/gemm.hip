@@ -621,6 +621,51 @@ int gemm_dispatch(const GemmArgs &g, int tile, hipStream_t st) {
   }
 }
 
+// ---- configurations in the tuning-cache vocabulary ------------------------
+// Variants, in order of preference: the DMA ring at 5 and 4 stages, then the
+// register-staged kernels.  vector_width 8 needs K % 8 == 0, N % 8 == 0 and
+// 16-byte aligned operands; 1 is the element-wise load path.
+enum GemmVariant { GV_DMA5, GV_DMA4, GV_REG256, GV_REG128, GV_REG64, GV_COUNT };
+
+pk_config gemm_variant_config(int v, int vw) {
+  switch (v) {
+    case GV_DMA5: return pk_config{G2_BM, G2_BN, G2_BK, G2_THREADS / 64, 8, G2_BK / 16, 5};
+    case GV_DMA4: return pk_config{G2_BM, G2_BN, G2_BK, G2_THREADS / 64, 8, G2_BK / 16, 4};
+    case GV_REG256: return pk_config{256, 256, BK, 8, vw, BK / 16, 2};
+    case GV_REG128: return pk_config{128, 128, BK, 4, vw, BK / 16, 2};
+    default: return pk_config{64, 64, BK, 4, vw, BK / 16, 2};
+  }
+}
+
+bool gemm_dma_shape_ok(int N, int K) {
+  return K % G2_BK == 0 && N % 8 == 0 && N >= 8 && (size_t)K * N * 2 < (size_t(1) << 31) &&
+         (size_t)G2_BM * K * 2 < (size_t(1) << 31);
+}
+
+bool cfg_matches(const pk_config &req, const pk_config &c) {
+  return (!req.block_m || req.block_m == c.block_m) && (!req.block_n || req.block_n == c.block_n) &&
+         (!req.block_k || req.block_k == c.block_k) && (!req.num_warps || req.num_warps == c.num_warps) &&
+         (!req.vector_width || req.vector_width == c.vector_width) && (!req.unroll || req.unroll == c.unroll) &&
+         (!req.shared_memory_stages || req.shared_memory_stages == c.shared_memory_stages);
+}
+
+template <int EPI>
+int gemm_launch_variant(const GemmArgs &g, int v, bool vec, hipStream_t st) {
+  switch (v) {
+    case GV_DMA5:
+      gemm_dma_kernel<EPI, 5><<<((g.M + G2_BM - 1) / G2_BM) * ((g.N + G2_BN - 1) / G2_BN), G2_THREADS, 0, st>>>(g);
+      PK_LAUNCH_CHECK("gemm_dma_kernel");
+      return PK_OK;
+    case GV_DMA4:
+      gemm_dma_kernel<EPI, 4><<<((g.M + G2_BM - 1) / G2_BM) * ((g.N + G2_BN - 1) / G2_BN), G2_THREADS, 0, st>>>(g);
+      PK_LAUNCH_CHECK("gemm_dma_kernel");
+      return PK_OK;
+    case GV_REG256: return launch_tile<256, 256, 2, 4, EPI>(g, vec, st);
+    case GV_REG128: return launch_tile<128, 128, 2, 2, EPI>(g, vec, st);
+    default: return launch_tile<64, 64, 2, 2, EPI>(g, vec, st);
+  }
+}
+
 // Largest tile that still gives at least ~one workgroup per CU.
 int pick_tile(int M, int N) {
   const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
@@ -631,6 +676,72 @@ int pick_tile(int M, int N) {
 }
 
 }  // namespace
+
+int gemm_configs(int M, int N, int K, pk_config *out, int cap) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int vw = (K % 8 == 0 && N % 8 == 0) ? 8 : 1;
+  int n = 0;
+  for (int v = 0; v < GV_COUNT; ++v) {
+    if ((v == GV_DMA5 || v == GV_DMA4) && !gemm_dma_shape_ok(N, K)) continue;
+    if (out && n < cap) out[n] = gemm_variant_config(v, vw);
+    ++n;
+    if (vw == 8 && v >= GV_REG256) {  // the element-wise load path is always there too
+      if (out && n < cap) out[n] = gemm_variant_config(v, 1);
+      ++n;
+    }
+  }
+  return n;
+}
+
+// What gemm_run picks for 16-byte aligned operands.
+bool gemm_default(int M, int N, int K, pk_config *out) {
+  if (M <= 0 || N <= 0 || K <= 0) return false;
+  const int vw = (K % 8 == 0 && N % 8 == 0) ? 8 : 1;
+  const int tile = pick_tile(M, N);
+  int v = tile == 0 ? GV_REG256 : tile == 1 ? GV_REG128 : GV_REG64;
+  if (tile == 0 && vw == 8 && gemm_dma_shape_ok(N, K)) v = g_ring_depth == 5 ? GV_DMA5 : GV_DMA4;
+  *out = gemm_variant_config(v, vw);
+  return true;
+}
+
+int gemm_run_config(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
+                    const uint16_t *R, int M, int N, int K, const pk_config &req, hipStream_t st) {
+  GemmArgs g{A, B, C, bias, R, nullptr, M, N, K};
+  const bool shape_vec = (K % 8 == 0) && (N % 8 == 0);
+  const bool ptr_vec = aligned16(A) && aligned16(B);
+  const bool ep_aligned = aligned16(C) && (!R || aligned16(R)) && (!bias || aligned16(bias));
+  int chosen = -1;
+  bool vec = false;
+  for (int v = 0; v < GV_COUNT && chosen < 0; ++v) {
+    if ((v == GV_DMA5 || v == GV_DMA4) && !(gemm_dma_shape_ok(N, K) && ptr_vec && ep_aligned)) continue;
+    for (int vw : {8, 1}) {
+      if (vw == 8 && !(shape_vec && ptr_vec)) continue;
+      if (vw == 1 && (v == GV_DMA5 || v == GV_DMA4)) continue;
+      if (cfg_matches(req, gemm_variant_config(v, vw))) {
+        chosen = v;
+        vec = vw == 8;
+        break;
+      }
+    }
+  }
+  if (chosen < 0) {
+    set_error("gemm: configuration {block_m %d, block_n %d, block_k %d, num_warps %d, vector_width %d, "
+              "unroll %d, stages %d} not available for M=%d N=%d K=%d with these operand alignments",
+              req.block_m, req.block_n, req.block_k, req.num_warps, req.vector_width, req.unroll,
+              req.shared_memory_stages, M, N, K);
+    return PK_ERR_UNSUPPORTED;
+  }
+  if (epi == EPI_BIAS_GELU) {
+    int rc = gelu_table(&g.gelu_tab);
+    if (rc) return rc;
+  }
+  switch (epi) {
+    case EPI_NONE: return gemm_launch_variant<EPI_NONE>(g, chosen, vec, st);
+    case EPI_BIAS_GELU: return gemm_launch_variant<EPI_BIAS_GELU>(g, chosen, vec, st);
+    case EPI_BIAS_RESID: return gemm_launch_variant<EPI_BIAS_RESID>(g, chosen, vec, st);
+    default: return gemm_launch_variant<EPI_RESID>(g, chosen, vec, st);
+  }
+}
 
 int gemm_run(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
              const uint16_t *R, int M, int N, int K, hipStream_t st, int tile = -1) {
@@ -930,6 +1041,24 @@ __global__ __launch_bounds__(RQ_THREADS) void rmsnorm_panel_gemm_fast_kernel(
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, int rows, int cols,
                    float eps, hipStream_t st);
 
+// The kernel fused_rmsnorm_matmul runs for aligned operands, as a config:
+// whole-K panel kernel (x panel and W slice in LDS, 4 waves); double-buffered
+// panel kernel (2 waves, 64-deep k-tiles); otherwise row normalisation into
+// workspace followed by the GEMM's own choice.
+bool rmsnorm_matmul_config(int M, int N, int K, pk_config *out) {
+  if (M <= 0 || N <= 0 || K <= 0) return false;
+  const bool panel_ok = (K % BK == 0) && K <= RP_MAX_K && (N % 8 == 0);
+  if (panel_ok && K <= RQ_MAX_K && (size_t)K * N * 2 < (size_t(1) << 31)) {
+    *out = pk_config{RQ_BM, RQ_BN, K, RQ_THREADS / 64, 8, K / 16, 1};
+    return true;
+  }
+  if (panel_ok) {
+    *out = pk_config{RP_BM, RP_BN, BK, RP_WAVES, 8, BK / 16, 2};
+    return true;
+  }
+  return gemm_default(M, N, K, out);
+}
+
 int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_t *W, uint16_t *out,
                          int M, int N, int K, float eps, hipStream_t st, const char *name) {
   PK_CHECK_ARG(x && W && out, "%s: null tensor pointer", name);
@@ -1046,6 +1175,17 @@ int pk_gemm_set_ring_depth(int depth) {
 // (0: 256x256 -- the DMA-pipelined kernel when K % 32 == 0 and the operands
 // are aligned, 1: 128x128, 2: 64x64, 3: the register-staged 256x256 kernel;
 // -1: heuristic).
+int pk_gemm_config_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
+                      const uint16_t *R, int M, int N, int K, const pk_config *cfg, void *stream) {
+  PK_CHECK_ARG(A && B && C, "pk_gemm_config_ex: null tensor pointer");
+  PK_CHECK_ARG(M > 0 && N > 0 && K > 0, "pk_gemm_config_ex: invalid shape");
+  PK_CHECK_ARG(epi >= 0 && epi <= 3, "pk_gemm_config_ex: epilogue %d not in 0..3", epi);
+  PK_CHECK_ARG((epi != EPI_BIAS_GELU || bias) && (epi < EPI_BIAS_RESID || R),
+               "pk_gemm_config_ex: epilogue %d needs its bias/residual operand", epi);
+  if (!cfg) return gemm_run(epi, A, B, C, bias, R, M, N, K, (hipStream_t)stream);
+  return gemm_run_config(epi, A, B, C, bias, R, M, N, K, *cfg, (hipStream_t)stream);
+}
+
 int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
                const uint16_t *R, int M, int N, int K, int tile, void *stream) {
   PK_CHECK_ARG(A && B && C, "pk_gemm_ex: null tensor pointer");

@@ -304,6 +304,9 @@ __global__ __launch_bounds__(256) void int8_reduce_kernel(Int8Args g) {
 // the split reduction) goes through the wave's own LDS region, one m-tile at
 // a time, with 16-byte global accesses.
 constexpr int I8S_KSTEP = 64;
+// Config fields fixed by the kernel's design: int8 elements per 16-byte DMA
+// lane, and 16x16x32 MFMA k-steps per 64-row ring step.
+constexpr int I8S_VECTOR_WIDTH = 16, I8S_UNROLL = I8S_KSTEP / 32;
 
 struct I8sArgs {
   const uint16_t *A;
@@ -624,7 +627,7 @@ double i8s_run_efficiency(int run, int waves) {
 // fp32 partials (written and read back) plus a second launch (counted as
 // ~24 MB of HBM time).  Fields of `req` that are nonzero are honoured;
 // returns false when nothing matches.
-bool i8s_plan(int M, int N, int K, const pk_int8_config *req, int cus, I8sPlan &best) {
+bool i8s_plan(int M, int N, int K, const pk_config *req, int cus, I8sPlan &best) {
   if (!i8s_shape_ok(M, N, K)) return false;
   const int ksteps = K / I8S_KSTEP;
   int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
@@ -633,6 +636,8 @@ bool i8s_plan(int M, int N, int K, const pk_int8_config *req, int cus, I8sPlan &
     mt = req->block_m / 16;
   }
   if (req && req->block_k && (req->block_k % I8S_KSTEP != 0 || req->block_k <= 0)) return false;
+  if (req && req->vector_width && req->vector_width != I8S_VECTOR_WIDTH) return false;
+  if (req && req->unroll && req->unroll != I8S_UNROLL) return false;
   double best_cost = 0;
   bool found = false;
   for (const I8sVariant &v : kI8s) {
@@ -677,7 +682,43 @@ size_t i8s_workspace(const I8sPlan &p, int M, int N) {
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
+pk_config i8s_config(const I8sVariant &v, int split_steps) {
+  return pk_config{16 * v.mt, 16 * v.nt * v.waves, split_steps * I8S_KSTEP, v.waves,
+                   I8S_VECTOR_WIDTH, I8S_UNROLL, v.stages};
+}
+
 }  // namespace
+
+// Every (variant, K split) the streaming kernel offers for the shape: row
+// blocks of 16, 32 or 64 up to M, each variant at every distinct split of
+// >= 4 ring steps per workgroup (as i8s_plan searches them).
+int int8_configs(int M, int N, int K, pk_config *out, int cap) {
+  if (M <= 0 || N <= 0 || K <= 0 || !i8s_shape_ok(M, N, K)) return 0;
+  const int ksteps = K / I8S_KSTEP;
+  const int mt_max = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  int n = 0;
+  for (const I8sVariant &v : kI8s) {
+    if (v.mt > mt_max) continue;
+    int last = -1;
+    static const int kSplits[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 28, 32};
+    for (int s : kSplits) {
+      const int split_steps = (ksteps + s - 1) / s;
+      if (s > 1 && split_steps < 4) break;
+      if (split_steps == last) continue;
+      last = split_steps;
+      if (n < cap && out) out[n] = i8s_config(v, split_steps);
+      ++n;
+    }
+  }
+  return n;
+}
+
+bool int8_default(int M, int N, int K, pk_config *out) {
+  I8sPlan p;
+  if (!i8s_plan(M, N, K, nullptr, device_cus(), p)) return false;
+  *out = i8s_config(*p.v, p.split_steps);
+  return true;
+}
 
 // Workspace for the built-in choice, whichever kernel the pointers' alignment
 // leads to.
@@ -700,7 +741,7 @@ static int use_workspace(size_t need, void *&ws, size_t ws_bytes) {
 }
 
 int int8_run(int epi, const uint16_t *A, const int8_t *W, const float *scale, uint16_t *C,
-             const uint16_t *R, int M, int N, int K, const pk_int8_config *cfg, void *ws,
+             const uint16_t *R, int M, int N, int K, const pk_config *cfg, void *ws,
              size_t ws_bytes, hipStream_t st) {
   const uint16_t *tab = nullptr;
   if (epi == I8_GELU) {
@@ -711,9 +752,11 @@ int int8_run(int epi, const uint16_t *A, const int8_t *W, const float *scale, ui
   const bool fast = aligned16(A) && aligned16(W) && aligned16(scale) && aligned16(C) &&
                     (epi != I8_RESID || aligned16(R)) && i8s_plan(M, N, K, cfg, device_cus(), plan);
   if (cfg && !fast) {
-    set_error("int8 matmul: configuration {block_m %d, block_n %d, block_k %d, num_warps %d, stages %d} "
-              "not available for M=%d N=%d K=%d",
-              cfg->block_m, cfg->block_n, cfg->block_k, cfg->num_warps, cfg->shared_memory_stages, M, N, K);
+    set_error("int8 matmul: configuration {block_m %d, block_n %d, block_k %d, num_warps %d, "
+              "vector_width %d, unroll %d, stages %d} not available for M=%d N=%d K=%d%s",
+              cfg->block_m, cfg->block_n, cfg->block_k, cfg->num_warps, cfg->vector_width, cfg->unroll,
+              cfg->shared_memory_stages, M, N, K,
+              i8s_shape_ok(M, N, K) ? "" : " (the shape or operand alignment needs the generic kernel)");
     return PK_ERR_UNSUPPORTED;
   }
   Int8Args g{A, W, scale, nullptr, C, R, tab, M, N, K, 1, 0};
@@ -785,23 +828,17 @@ int launch_matmul_int8(const uint16_t *A, const int8_t *Wq, const float *scale, 
   return int8_run(I8_NONE, A, Wq, scale, C, nullptr, M, N, K, nullptr, nullptr, 0, (hipStream_t)stream);
 }
 
-int pk_int8_default_config(int M, int N, int K, pk_int8_config *out) {
+int pk_int8_default_config(int M, int N, int K, pk_config *out) {
   PK_CHECK_ARG(out && M > 0 && N > 0 && K > 0, "pk_int8_default_config: invalid argument");
-  I8sPlan p;
-  if (!i8s_plan(M, N, K, nullptr, device_cus(), p)) {
+  if (!int8_default(M, N, K, out)) {
     set_error("pk_int8_default_config: M=%d N=%d K=%d takes the generic kernel", M, N, K);
     return PK_ERR_UNSUPPORTED;
   }
-  out->block_m = 16 * p.v->mt;
-  out->block_n = 16 * p.v->nt * p.v->waves;
-  out->block_k = p.split_steps * I8S_KSTEP;
-  out->num_warps = p.v->waves;
-  out->shared_memory_stages = p.v->stages;
   return PK_OK;
 }
 
 int pk_matmul_int8_ex(int epi, const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C,
-                      const uint16_t *R, int M, int N, int K, const pk_int8_config *cfg,
+                      const uint16_t *R, int M, int N, int K, const pk_config *cfg,
                       void *workspace, size_t workspace_bytes, void *stream) {
   PK_CHECK_ARG(epi >= I8_NONE && epi <= I8_RESID, "pk_matmul_int8_ex: epilogue %d not in 0..2", epi);
   PK_CHECK_ARG(A && Wq && scale && C && (epi != I8_RESID || R), "pk_matmul_int8_ex: null tensor pointer");

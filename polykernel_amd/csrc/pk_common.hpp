@@ -55,6 +55,18 @@ int gelu_table(const uint16_t **table);
 // Library-owned per-device scratch for entry points without a workspace arg.
 int library_workspace(size_t bytes, void **ptr);
 
+// Configurations in the tuning-cache vocabulary (each defined beside the
+// dispatcher it describes).  *_configs write min(total, cap) entries and
+// return the total; the bool functions describe the built-in choice.
+int gemm_configs(int M, int N, int K, pk_config *out, int cap);
+bool gemm_default(int M, int N, int K, pk_config *out);
+int int8_configs(int M, int N, int K, pk_config *out, int cap);
+bool int8_default(int M, int N, int K, pk_config *out);
+bool rmsnorm_matmul_config(int M, int N, int K, pk_config *out);
+bool rmsnorm_config(int rows, int cols, pk_config *out);
+bool softmax_config(int rows, int cols, pk_config *out);
+bool attention_config(int S_q, int S_kv, int D, pk_config *out);
+
 // ---- device helpers ------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 

@@ -469,6 +469,38 @@ int kv_append_inplace_launch(uint16_t *cache, const uint16_t *neu, int64_t BH, i
   return PK_OK;
 }
 
+// The kernels the row-wise dispatchers above run for 16-byte aligned
+// operands, as configs: block_m = rows per workgroup (4: one wave per row;
+// 1: four waves per row), block_n = cols, num_warps = 4, vector_width = bf16
+// per load (8, or 1 for the generic kernel), unroll = 16-byte vectors per
+// lane, one pass over a register-resident row (block_k 0, stages 1).
+bool rmsnorm_config(int rows, int cols, pk_config *out) {
+  if (rows <= 0 || cols <= 0) return false;
+  const int nvec = cols / 8;
+  if (cols % 8 == 0 && nvec <= 64 * 8) {
+    const int vpt = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : 8;
+    *out = pk_config{4, cols, 0, kBlock / 64, 8, vpt, 1};
+  } else if (cols % 8 == 0 && nvec <= 256 * 8) {
+    *out = pk_config{1, cols, 0, kBlock / 64, 8, nvec <= 256 * 4 ? 4 : 8, 1};
+  } else {
+    *out = pk_config{1, cols, 0, kBlock / 64, 1, 1, 1};
+  }
+  return true;
+}
+
+bool softmax_config(int rows, int cols, pk_config *out) {
+  if (rows <= 0 || cols <= 0) return false;
+  const int nvec = cols / 8;
+  if (cols % 8 == 0 && nvec <= 64 * 4) {
+    *out = pk_config{4, cols, 0, kBlock / 64, 8, nvec <= 64 ? 1 : nvec <= 128 ? 2 : 4, 1};
+  } else if (cols % 8 == 0 && nvec <= 256 * 8) {
+    *out = pk_config{1, cols, 0, kBlock / 64, 8, nvec <= 256 * 2 ? 2 : nvec <= 256 * 4 ? 4 : 8, 1};
+  } else {
+    *out = pk_config{1, cols, 0, kBlock / 64, 1, 1, 1};
+  }
+  return true;
+}
+
 }  // namespace pk
 
 using namespace pk;

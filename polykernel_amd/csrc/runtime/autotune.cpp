@@ -1,0 +1,455 @@
+// autotune.cpp -- the correctness-gated sweep that writes gfx950 tuning
+// entries.
+//
+// Invariant (lib/Autotune/Benchmark.h:7-12 of the reference): a variant is
+// timed only after it passed the correctness gate, and the winner is the
+// fastest validated variant (SelectBestValidated); a variant that fails the
+// gate is recorded as not validated and is never best.
+//
+// For one (op, shape) on the current device:
+//   1. seeded synthetic inputs of the op's documented distributions are made
+//      on the host (pk_synth_*, the generator bench.py uses) and uploaded;
+//   2. the naive device golden of the op (pk_naive_*) computes the expected
+//      output once;
+//   3. every candidate of ConfigSpace::Candidates -- the library's default
+//      first -- runs once into an output poisoned with NaN, is compared with
+//      the golden (pk_compare_bf16: cosine, max_rel_err, pcc) and gated;
+//   4. a variant that passes is timed with HIP events, `warmup` launches
+//      then the median of `iters`, rotating over copies of its inputs large
+//      enough that the 256 MiB MALL cannot hold them (HBM-bound kernels would
+//      otherwise be timed from cache);
+//   5. the fastest validated variant becomes the entry (scored_by
+//      "measure", time_ms its median).
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <functional>
+
+#include "../../../include/polykernel_amd_runtime.hpp"
+
+namespace pk::autotune {
+
+namespace {
+
+bool HipOk(hipError_t e, const char *what, std::string &error) {
+  if (e == hipSuccess) return true;
+  error = std::string(what) + ": " + hipGetErrorString(e);
+  (void)hipGetLastError();
+  return false;
+}
+
+bool PkOk(int rc, const char *what, std::string &error) {
+  if (rc == PK_OK) return true;
+  error = std::string(what) + " failed (status " + std::to_string(rc) + "): " + pk_last_error();
+  return false;
+}
+
+// Device allocations of one sweep, freed together.
+class DeviceArena {
+ public:
+  DeviceArena() = default;
+  DeviceArena(const DeviceArena &) = delete;
+  DeviceArena &operator=(const DeviceArena &) = delete;
+  ~DeviceArena() {
+    for (void *p : ptrs_) (void)hipFree(p);
+  }
+  template <typename T>
+  T *Alloc(size_t count, std::string &error) {
+    void *p = nullptr;
+    if (!HipOk(hipMalloc(&p, std::max<size_t>(count * sizeof(T), 256)), "hipMalloc", error)) return nullptr;
+    ptrs_.push_back(p);
+    return static_cast<T *>(p);
+  }
+
+ private:
+  std::vector<void *> ptrs_;
+};
+
+template <typename T>
+bool Upload(T *dst, const std::vector<T> &src, std::string &error) {
+  return HipOk(hipMemcpy(dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D", error);
+}
+
+std::vector<uint16_t> NormalBf16(size_t n, uint64_t seed, uint64_t stream, double std_dev, double mean = 0.0) {
+  std::vector<uint16_t> v(n);
+  pk_synth_normal_bf16(seed, stream, mean, std_dev, v.data(), (int64_t)n);
+  return v;
+}
+
+// A prepared sweep: run(variant, copy) launches one candidate on one copy of
+// the inputs; golden() writes the expected output; the gate compares the
+// first `compare_n` elements of out[0] and want.
+struct Workload {
+  std::function<int(const pk_config *, int, hipStream_t)> run;
+  std::function<int(hipStream_t)> golden;
+  std::vector<uint16_t *> out;
+  size_t out_elems = 0;
+  const uint16_t *want = nullptr;
+  long long compare_n = 0;
+  int copies = 1;
+};
+
+int CopiesFor(size_t input_bytes, const AutotuneOptions &o) {
+  if (input_bytes == 0) return 1;
+  const size_t c = (o.rotate_bytes + input_bytes - 1) / input_bytes;
+  return (int)std::clamp<size_t>(c, 1, 4);
+}
+
+// Replicate copy 0 of a device buffer into copies 1..n-1.
+template <typename T>
+bool Replicate(std::vector<T *> &bufs, size_t count, std::string &error) {
+  for (size_t i = 1; i < bufs.size(); ++i)
+    if (!HipOk(hipMemcpy(bufs[i], bufs[0], count * sizeof(T), hipMemcpyDeviceToDevice), "hipMemcpy D2D", error))
+      return false;
+  return true;
+}
+
+template <typename T>
+bool AllocCopies(DeviceArena &arena, std::vector<T *> &bufs, int copies, size_t count, std::string &error) {
+  bufs.assign(copies, nullptr);
+  for (int i = 0; i < copies; ++i)
+    if (!(bufs[i] = arena.Alloc<T>(count, error))) return false;
+  return true;
+}
+
+bool PrepareGemm(std::string_view op, const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
+                 std::string &error) {
+  const int epi = op == "matmul" ? 0 : op == "fused_matmul_bias_gelu" ? 1 : 2;
+  const int M = (int)s.m, N = (int)s.n, K = (int)s.k;
+  const size_t a_n = (size_t)M * K, b_n = (size_t)K * N, c_n = (size_t)M * N;
+  const size_t in_bytes = 2 * (a_n + b_n + (epi == 2 ? c_n : 0));
+  w.copies = CopiesFor(in_bytes, o);
+  std::vector<uint16_t *> A, B, R, bias;
+  if (!AllocCopies(arena, A, w.copies, a_n, error) || !AllocCopies(arena, B, w.copies, b_n, error) ||
+      !AllocCopies(arena, bias, w.copies, N, error) || !AllocCopies(arena, w.out, w.copies, c_n, error))
+    return false;
+  if (epi == 2 && !AllocCopies(arena, R, w.copies, c_n, error)) return false;
+  if (!Upload(A[0], NormalBf16(a_n, o.seed, 1, 1.0), error) ||
+      !Upload(B[0], NormalBf16(b_n, o.seed, 3, 1.0 / std::sqrt((double)K)), error) ||
+      !Upload(bias[0], NormalBf16(N, o.seed, 4, 0.02), error))
+    return false;
+  if (epi == 2 && !Upload(R[0], NormalBf16(c_n, o.seed, 5, 1.0), error)) return false;
+  if (!Replicate(A, a_n, error) || !Replicate(B, b_n, error) || !Replicate(bias, N, error)) return false;
+  if (epi == 2 && !Replicate(R, c_n, error)) return false;
+  uint16_t *want = arena.Alloc<uint16_t>(c_n, error);
+  if (!want) return false;
+  w.want = want;
+  w.out_elems = c_n;
+  w.compare_n = (long long)c_n;
+  const uint16_t *b1 = epi == 0 ? nullptr : bias[0];
+  w.golden = [=](hipStream_t st) {
+    return pk_naive_matmul(epi == 2 ? 2 : epi, A[0], B[0], want, b1, epi == 2 ? R[0] : nullptr, M, N, K, st);
+  };
+  w.run = [=](const pk_config *cfg, int c, hipStream_t st) {
+    return pk_gemm_config_ex(epi, A[c], B[c], w.out[c], epi == 0 ? nullptr : bias[c], epi == 2 ? R[c] : nullptr, M,
+                             N, K, cfg, st);
+  };
+  return true;
+}
+
+bool PrepareInt8(std::string_view op, const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
+                 std::string &error) {
+  const int epi = op == "matmul_int8" ? 0 : op == "matmul_int8_gelu" ? 1 : 2;
+  const int M = (int)s.m, N = (int)s.n, K = (int)s.k;
+  const size_t a_n = (size_t)M * K, w_n = (size_t)K * N, c_n = (size_t)M * N;
+  w.copies = CopiesFor(w_n + 4 * (size_t)N + 2 * a_n, o);
+  std::vector<uint16_t *> A, R;
+  std::vector<int8_t *> Wq;
+  std::vector<float *> scale;
+  if (!AllocCopies(arena, A, w.copies, a_n, error) || !AllocCopies(arena, Wq, w.copies, w_n, error) ||
+      !AllocCopies(arena, scale, w.copies, N, error) || !AllocCopies(arena, w.out, w.copies, c_n, error))
+    return false;
+  if (epi == 2 && !AllocCopies(arena, R, w.copies, c_n, error)) return false;
+  {
+    // bf16 weights N(0, 1/K), quantised on the device
+    uint16_t *wb = arena.Alloc<uint16_t>(w_n, error);
+    if (!wb || !Upload(wb, NormalBf16(w_n, o.seed, 3, 1.0 / std::sqrt((double)K)), error)) return false;
+    if (!PkOk(launch_quantize_int8_per_channel(wb, Wq[0], scale[0], K, N, nullptr), "quantize", error)) return false;
+    if (!HipOk(hipDeviceSynchronize(), "quantize", error)) return false;
+  }
+  if (!Upload(A[0], NormalBf16(a_n, o.seed, 1, 1.0), error)) return false;
+  if (epi == 2 && !Upload(R[0], NormalBf16(c_n, o.seed, 5, 1.0), error)) return false;
+  if (!Replicate(A, a_n, error) || !Replicate(Wq, w_n, error) || !Replicate(scale, N, error)) return false;
+  if (epi == 2 && !Replicate(R, c_n, error)) return false;
+  uint16_t *want = arena.Alloc<uint16_t>(c_n, error);
+  if (!want) return false;
+  w.want = want;
+  w.out_elems = c_n;
+  w.compare_n = (long long)c_n;
+  w.golden = [=](hipStream_t st) {
+    return pk_naive_matmul_int8(epi, A[0], Wq[0], scale[0], want, epi == 2 ? R[0] : nullptr, M, N, K, st);
+  };
+  w.run = [=](const pk_config *cfg, int c, hipStream_t st) {
+    return pk_matmul_int8_ex(epi, A[c], Wq[c], scale[c], w.out[c], epi == 2 ? R[c] : nullptr, M, N, K, cfg, nullptr,
+                             0, st);
+  };
+  return true;
+}
+
+bool PrepareRmsnormMatmul(const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
+                          std::string &error) {
+  const int M = (int)s.m, N = (int)s.n, K = (int)s.k;
+  const size_t x_n = (size_t)M * K, w_n = (size_t)K * N, c_n = (size_t)M * N;
+  w.copies = CopiesFor(2 * (x_n + w_n), o);
+  std::vector<uint16_t *> X, W, G;
+  if (!AllocCopies(arena, X, w.copies, x_n, error) || !AllocCopies(arena, W, w.copies, w_n, error) ||
+      !AllocCopies(arena, G, w.copies, K, error) || !AllocCopies(arena, w.out, w.copies, c_n, error))
+    return false;
+  if (!Upload(X[0], NormalBf16(x_n, o.seed, 11, 1.0), error) ||
+      !Upload(G[0], NormalBf16(K, o.seed, 12, 0.1, 1.0), error) ||
+      !Upload(W[0], NormalBf16(w_n, o.seed, 13, 1.0 / std::sqrt((double)K)), error))
+    return false;
+  if (!Replicate(X, x_n, error) || !Replicate(W, w_n, error) || !Replicate(G, K, error)) return false;
+  uint16_t *want = arena.Alloc<uint16_t>(c_n, error), *normed = arena.Alloc<uint16_t>(x_n, error);
+  if (!want || !normed) return false;
+  w.want = want;
+  w.out_elems = c_n;
+  w.compare_n = (long long)c_n;
+  w.golden = [=](hipStream_t st) {
+    const int rc = pk_naive_rmsnorm(X[0], nullptr, G[0], normed, M, K, 1e-6f, st);
+    return rc ? rc : pk_naive_matmul(0, normed, W[0], want, nullptr, nullptr, M, N, K, st);
+  };
+  w.run = [=](const pk_config *, int c, hipStream_t st) {
+    return launch_fused_rmsnorm_matmul_gamma(X[c], G[c], W[c], w.out[c], M, N, K, 1e-6f, st);
+  };
+  return true;
+}
+
+bool PrepareResidualRmsnorm(const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
+                            std::string &error) {
+  const int rows = (int)s.m, cols = (int)s.n;
+  const size_t n = (size_t)rows * cols;
+  w.copies = CopiesFor(4 * n, o);
+  std::vector<uint16_t *> X, R, G;
+  if (!AllocCopies(arena, X, w.copies, n, error) || !AllocCopies(arena, R, w.copies, n, error) ||
+      !AllocCopies(arena, G, w.copies, cols, error) || !AllocCopies(arena, w.out, w.copies, n, error))
+    return false;
+  if (!Upload(X[0], NormalBf16(n, o.seed, 31, 1.0), error) || !Upload(R[0], NormalBf16(n, o.seed, 32, 1.0), error) ||
+      !Upload(G[0], NormalBf16(cols, o.seed, 33, 0.1, 1.0), error))
+    return false;
+  if (!Replicate(X, n, error) || !Replicate(R, n, error) || !Replicate(G, cols, error)) return false;
+  uint16_t *want = arena.Alloc<uint16_t>(n, error);
+  if (!want) return false;
+  w.want = want;
+  w.out_elems = n;
+  w.compare_n = (long long)n;
+  w.golden = [=](hipStream_t st) { return pk_naive_rmsnorm(X[0], R[0], G[0], want, rows, cols, 1e-6f, st); };
+  w.run = [=](const pk_config *, int c, hipStream_t st) {
+    return launch_fused_residual_rmsnorm(X[c], R[c], G[c], w.out[c], rows, cols, 1e-6f, st);
+  };
+  return true;
+}
+
+bool PrepareSoftmaxMask(const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
+                        std::string &error) {
+  const int rows = (int)s.m, cols = (int)s.n;
+  const size_t n = (size_t)rows * cols;
+  w.copies = CopiesFor(6 * n, o);
+  std::vector<float *> L;
+  std::vector<uint16_t *> Mk;
+  if (!AllocCopies(arena, L, w.copies, n, error) || !AllocCopies(arena, Mk, w.copies, n, error) ||
+      !AllocCopies(arena, w.out, w.copies, n, error))
+    return false;
+  {
+    std::vector<float> l(n);
+    pk_synth_normal_f32(o.seed, 34, 0.0, 2.0, l.data(), (int64_t)n);
+    std::vector<uint16_t> m(n);
+    pk_synth_mask_bf16(o.seed, 35, 0.1, m.data(), (int64_t)n);
+    if (!Upload(L[0], l, error) || !Upload(Mk[0], m, error)) return false;
+  }
+  if (!Replicate(L, n, error) || !Replicate(Mk, n, error)) return false;
+  uint16_t *want = arena.Alloc<uint16_t>(n, error);
+  if (!want) return false;
+  w.want = want;
+  w.out_elems = n;
+  w.compare_n = (long long)n;
+  w.golden = [=](hipStream_t st) { return pk_naive_softmax_mask(L[0], Mk[0], want, rows, cols, st); };
+  w.run = [=](const pk_config *, int c, hipStream_t st) {
+    return launch_fused_softmax_mask(L[c], Mk[c], w.out[c], rows, cols, st);
+  };
+  return true;
+}
+
+// Shape {S_q, S_kv, D}; B = 1, H = batch_heads; the cache holds S_kv - S_q
+// rows and room for S_kv.  The cache rows at [S_cache, S_kv) are pre-filled
+// with the new rows, so the in-place append writes what is already there and
+// every launch sees the same inputs.  The golden covers the first two heads.
+bool PrepareAttention(const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
+                      std::string &error) {
+  const int Sq = (int)s.m, Skv = (int)s.n, D = (int)s.k, BH = std::max(1, o.batch_heads);
+  const int Sc = Skv - Sq;
+  if (Sc < 0 || D <= 0 || D > 128) {
+    error = "fused_kv_append_attention: shape needs S_kv >= S_q and 0 < D <= 128";
+    return false;
+  }
+  const size_t q_n = (size_t)BH * Sq * D, kv_n = (size_t)BH * Skv * D;
+  w.copies = CopiesFor(4 * kv_n + 2 * q_n, o);
+  std::vector<uint16_t *> Kc, Vc;
+  uint16_t *Q = arena.Alloc<uint16_t>(q_n, error), *Kn = arena.Alloc<uint16_t>(q_n, error),
+           *Vn = arena.Alloc<uint16_t>(q_n, error);
+  if (!Q || !Kn || !Vn || !AllocCopies(arena, Kc, w.copies, kv_n, error) ||
+      !AllocCopies(arena, Vc, w.copies, kv_n, error) || !AllocCopies(arena, w.out, w.copies, q_n, error))
+    return false;
+  const std::vector<uint16_t> q = NormalBf16(q_n, o.seed, 21, 1.0), kn = NormalBf16(q_n, o.seed, 22, 1.0),
+                              vn = NormalBf16(q_n, o.seed, 23, 1.0);
+  std::vector<uint16_t> kc(kv_n), vc(kv_n);
+  {
+    const std::vector<uint16_t> kold = NormalBf16((size_t)BH * Sc * D, o.seed, 24, 1.0),
+                                vold = NormalBf16((size_t)BH * Sc * D, o.seed, 25, 1.0);
+    for (int bh = 0; bh < BH; ++bh) {
+      std::copy_n(kold.begin() + (size_t)bh * Sc * D, (size_t)Sc * D, kc.begin() + (size_t)bh * Skv * D);
+      std::copy_n(vold.begin() + (size_t)bh * Sc * D, (size_t)Sc * D, vc.begin() + (size_t)bh * Skv * D);
+      std::copy_n(kn.begin() + (size_t)bh * Sq * D, (size_t)Sq * D, kc.begin() + ((size_t)bh * Skv + Sc) * D);
+      std::copy_n(vn.begin() + (size_t)bh * Sq * D, (size_t)Sq * D, vc.begin() + ((size_t)bh * Skv + Sc) * D);
+    }
+  }
+  if (!Upload(Q, q, error) || !Upload(Kn, kn, error) || !Upload(Vn, vn, error) || !Upload(Kc[0], kc, error) ||
+      !Upload(Vc[0], vc, error))
+    return false;
+  if (!Replicate(Kc, kv_n, error) || !Replicate(Vc, kv_n, error)) return false;
+  const int heads = std::min(BH, 2);
+  uint16_t *want = arena.Alloc<uint16_t>((size_t)heads * Sq * D, error);
+  if (!want) return false;
+  const float scale = 1.0f / std::sqrt((float)D);
+  w.want = want;
+  w.out_elems = q_n;
+  w.compare_n = (long long)heads * Sq * D;
+  w.golden = [=](hipStream_t st) {
+    return pk_naive_attention(Q, Kc[0], Vc[0], want, heads, Sq, Skv, Skv, D, scale, 1, st);
+  };
+  w.run = [=](const pk_config *, int c, hipStream_t st) {
+    return launch_fused_kv_append_attention(Q, Kc[c], Vc[c], Kn, Vn, w.out[c], 1, BH, Sq, Sc, D, Skv, scale, 1, st);
+  };
+  return true;
+}
+
+bool Prepare(std::string_view op, const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
+             std::string &error) {
+  if (s.m > INT32_MAX || s.n > INT32_MAX || s.k > INT32_MAX || s.m <= 0 || s.n <= 0 || s.k < 0) {
+    error = "shape out of range";
+    return false;
+  }
+  if (op == "matmul" || op == "fused_matmul_bias_gelu" || op == "fused_matmul_bias_residual")
+    return PrepareGemm(op, s, o, arena, w, error);
+  if (op == "matmul_int8" || op == "matmul_int8_gelu" || op == "matmul_int8_residual")
+    return PrepareInt8(op, s, o, arena, w, error);
+  if (op == "fused_rmsnorm_matmul") return PrepareRmsnormMatmul(s, o, arena, w, error);
+  if (op == "fused_residual_rmsnorm") return PrepareResidualRmsnorm(s, o, arena, w, error);
+  if (op == "fused_softmax_mask") return PrepareSoftmaxMask(s, o, arena, w, error);
+  if (op == "fused_kv_append_attention") return PrepareAttention(s, o, arena, w, error);
+  error = "autotune: unknown op " + std::string(op);
+  return false;
+}
+
+pk_config ToPk(const Config &c) {
+  return pk_config{c.block_m, c.block_n, c.block_k, c.num_warps, c.vector_width, c.unroll, c.shared_memory_stages};
+}
+
+}  // namespace
+
+bool Autotune(std::string_view op, const Shape &shape, const AutotuneOptions &o, AutotuneResult &result,
+              std::string &error) {
+  result = AutotuneResult{};
+  const std::optional<runtime::DeviceInfo> dev = runtime::HipDeviceDetector().Detect();
+  if (!dev) {
+    error = "autotune: no usable GPU";
+    return false;
+  }
+  std::vector<Config> cands = ConfigSpace::Candidates(op, shape);
+  if (cands.empty()) {
+    error = "autotune: no configuration of the gfx950 kernels accepts " + runtime::FormatKey(dev->arch, op, shape);
+    return false;
+  }
+  if (const std::optional<Config> def = ConfigSpace::Default(op, shape)) {
+    const auto it = std::find(cands.begin(), cands.end(), *def);
+    if (it != cands.end()) std::rotate(cands.begin(), it, it + 1);  // the built-in choice first
+  }
+  if (o.max_variants && cands.size() > *o.max_variants) cands.resize(std::max<size_t>(1, *o.max_variants));
+  const double ceiling = o.rel_ceiling ? *o.rel_ceiling : RelCeiling(op, shape.k);
+
+  DeviceArena arena;
+  Workload w;
+  if (!Prepare(op, shape, o, arena, w, error)) return false;
+  hipStream_t st = nullptr;
+  if (!HipOk(hipStreamCreate(&st), "hipStreamCreate", error)) return false;
+  struct StreamGuard {
+    hipStream_t s;
+    ~StreamGuard() { (void)hipStreamDestroy(s); }
+  } guard{st};
+  if (!PkOk(w.golden(st), "golden", error) || !HipOk(hipStreamSynchronize(st), "golden", error)) return false;
+
+  std::vector<VariantResult> results;
+  for (const Config &c : cands) {
+    VariantResult v;
+    v.name = ToString(c);
+    const pk_config pc = ToPk(c);
+    // poison: an element the variant does not write reads as NaN and fails
+    bool ok = HipOk(hipMemsetAsync(w.out[0], 0xFF, w.out_elems * 2, st), "hipMemsetAsync", error);
+    int rc = ok ? w.run(&pc, 0, st) : PK_ERR_HIP;
+    ok = ok && rc == PK_OK && HipOk(hipStreamSynchronize(st), "variant", error);
+    double m[4] = {0, 0, 0, 0};
+    if (ok) ok = pk_compare_bf16(w.out[0], w.want, w.compare_n, m, st) == PK_OK;
+    if (!ok) {
+      if (o.verbose) std::fprintf(stderr, "[autotune] %s: launch failed: %s\n", v.name.c_str(), pk_last_error());
+      (void)hipGetLastError();
+      error.clear();
+      v.correctness = Correctness{0.0, INFINITY, 0.0};
+      results.push_back(v);
+      continue;
+    }
+    v.correctness = Correctness{m[0], m[1], m[2]};
+    v.validated = PassesCorrectnessGate(v.correctness, ceiling);
+    if (v.validated) {
+      for (int i = 0; i < o.warmup; ++i) (void)w.run(&pc, i % w.copies, st);
+      std::vector<float> times;
+      for (int i = 0; i < std::max(1, o.iters); ++i) {
+        HipEventTimer t;
+        t.Start(st);
+        rc = w.run(&pc, i % w.copies, st);
+        t.Stop(st);
+        const float ms = t.ElapsedMs();
+        if (rc != PK_OK || ms < 0) {
+          v.validated = false;
+          break;
+        }
+        times.push_back(ms);
+      }
+      if (v.validated) {
+        std::sort(times.begin(), times.end());
+        v.time_ms = times[times.size() / 2];
+      }
+    }
+    if (o.verbose)
+      std::fprintf(stderr, "[autotune] %s %s cosine=%.6f max_rel=%.3e pcc=%.6f %s%s\n", std::string(op).c_str(),
+                   v.name.c_str(), m[0], m[1], m[2], v.validated ? "PASS" : "REJECTED",
+                   v.time_ms ? (" " + std::to_string(*v.time_ms) + " ms").c_str() : "");
+    results.push_back(v);
+  }
+  if (!HipOk(hipStreamSynchronize(st), "sweep", error)) return false;
+
+  const std::optional<size_t> best = SelectBestValidated(results);
+  const size_t pick = best ? *best : 0;
+  CacheEntry &e = result.entry;
+  e.gpu = dev->arch;
+  e.op = std::string(op);
+  e.shape = shape;
+  e.best = cands[pick];
+  e.scored_by = "measure";
+  e.time_ms = best ? results[pick].time_ms : std::nullopt;
+  e.validated = best.has_value();
+  // JSON has no NaN or infinity: a failed comparison is recorded as the
+  // worst finite value of each metric
+  for (VariantResult &v : results) {
+    Correctness &c = v.correctness;
+    if (!std::isfinite(c.cosine)) c.cosine = 0.0;
+    if (!std::isfinite(c.pcc)) c.pcc = 0.0;
+    if (!std::isfinite(c.max_rel_err)) c.max_rel_err = 1e308;
+  }
+  e.correctness = results[pick].correctness;
+  for (size_t i = 0; i < cands.size(); ++i) result.variants.emplace_back(cands[i], results[i]);
+  return true;
+}
+
+}  // namespace pk::autotune

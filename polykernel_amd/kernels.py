@@ -241,7 +241,7 @@ def matmul_int8(a: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor) -> torch
 
 def int8_default_config(M: int, N: int, K: int) -> Optional[dict]:
     """Configuration launch_matmul_int8 picks for a shape (None: generic kernel)."""
-    cfg = _lib.Int8Config()
+    cfg = _lib.Config()
     rc = _lib.load().pk_int8_default_config(M, N, K, cfg)
     if rc == _lib.PK_ERR_UNSUPPORTED:
         return None
@@ -256,7 +256,7 @@ def matmul_int8_ex(epi: int, a: torch.Tensor, wq: torch.Tensor, scale: torch.Ten
     K = a.shape[-1]
     M, N = a.numel() // K, wq.shape[1]
     out = torch.empty(*a.shape[:-1], N, dtype=bf16, device=a.device)
-    cfg = None if config is None else _lib.Int8Config(**config)
+    cfg = None if config is None else _lib.Config(**config)
     check(_lib.load().pk_matmul_int8_ex(epi, _dev(a, bf16, "a"), _dev(wq, torch.int8, "wq"),
                                         _dev(scale, torch.float32, "scale"), _dev(out, bf16, "out"),
                                         _opt(residual, bf16, "residual"), M, N, K, cfg, None, 0,

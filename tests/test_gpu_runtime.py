@@ -1,0 +1,293 @@
+"""GPU tests of the tuning path: every configuration the kernels list runs and
+is exact, the naive device goldens the autotuner gates against agree with the
+C oracle, the device metrics agree with polykernel_amd.metrics, the autotuner
+gates before it times, and Runtime::Run serves a tuned entry through the
+C-ABI with the same bits as a direct call."""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import math
+
+import numpy as np
+import pytest
+
+from polykernel_amd import _lib
+from polykernel_amd import metrics as mt
+from polykernel_amd import runtime as rt
+from polykernel_amd import synth
+from tests.helpers import bf, f32, from_dev, int_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _empty_bf16(shape):
+    import torch
+
+    return torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+
+
+def _cfg(d):
+    return _lib.Config(**d)
+
+
+def gemm_cfg(epi, a, b, cfg, bias=None, r=None):
+    M, Kd = a.shape
+    N = b.shape[1]
+    out = _empty_bf16((M, N))
+    c = _cfg(cfg)
+    _lib.check(_lib.load().pk_gemm_config_ex(epi, _ptr(a), _ptr(b), _ptr(out), _ptr(bias), _ptr(r), M, N, Kd,
+                                             C.byref(c), _stream()), "pk_gemm_config_ex")
+    return out
+
+
+# ------------------------------------------------------------------ every listed config runs
+
+@pytest.mark.parametrize("M,N,Kd", [(256, 512, 256), (130, 127, 65), (512, 264, 1056)])
+def test_every_gemm_config_bit_exact_on_integer_inputs(gpu, oracle, M, N, Kd):
+    a, b = int_bf16((M, Kd), 61), int_bf16((Kd, N), 62)
+    want = oracle.matmul(a, b)
+    cands = rt.candidates("matmul", M, N, Kd)
+    assert cands
+    for cfg in cands:
+        _say(f"gemm {M}x{N}x{Kd} {cfg}")
+        got = from_dev(gemm_cfg(0, to_dev(a), to_dev(b), cfg))
+        assert np.array_equal(got, want), cfg
+
+
+@pytest.mark.parametrize("epi", [1, 2])
+def test_every_gemm_config_epilogues_bit_exact(gpu, oracle, epi):
+    M, N, Kd = 256, 512, 512
+    a, b = int_bf16((M, Kd), 63), int_bf16((Kd, N), 64)
+    bias = synth.normal_bf16((N,), 65, 0.5)
+    r = synth.normal_bf16((M, N), 66)
+    if epi == 1:
+        want = oracle.fused_matmul_bias_gelu(a, b, bias)
+    else:
+        want = oracle.fused_matmul_bias_residual(a, b, bias, r)
+    for cfg in rt.candidates("fused_matmul_bias_gelu", M, N, Kd):
+        _say(f"gemm epi {epi} {cfg}")
+        got = from_dev(gemm_cfg(epi, to_dev(a), to_dev(b), cfg, bias=to_dev(bias), r=to_dev(r) if epi == 2 else None))
+        assert np.array_equal(got, want), cfg
+
+
+def test_gemm_config_unavailable_is_an_error(gpu):
+    a, b = to_dev(int_bf16((64, 64), 1)), to_dev(int_bf16((64, 64), 2))
+    cfg = dict(block_m=96, block_n=96, block_k=32, num_warps=4, vector_width=8, unroll=2, shared_memory_stages=5)
+    with pytest.raises(_lib.PolyKernelError) as ei:
+        gemm_cfg(0, a, b, cfg)
+    assert ei.value.code == _lib.PK_ERR_UNSUPPORTED
+    # the DMA ring needs K % 32 == 0: asking for it at K = 72 is refused, not run
+    a2, b2 = to_dev(int_bf16((64, 72), 3)), to_dev(int_bf16((72, 64), 4))
+    dma = dict(block_m=256, block_n=256, block_k=32, num_warps=4, vector_width=8, unroll=2, shared_memory_stages=5)
+    with pytest.raises(_lib.PolyKernelError):
+        gemm_cfg(0, a2, b2, dma)
+
+
+def test_every_int8_config_bit_exact(gpu, oracle):
+    from polykernel_amd import kernels
+
+    M, N, Kd = 16, 1024, 2048
+    a = int_bf16((M, Kd), 67)
+    wq = np.random.default_rng(68).integers(-127, 128, size=(Kd, N)).astype(np.int8)
+    s = (2.0 ** np.random.default_rng(69).integers(-8, -2, size=N)).astype(np.float32)
+    want = oracle.matmul_int8(a, wq, s)
+    cands = rt.candidates("matmul_int8", M, N, Kd)
+    assert len(cands) > 20
+    for cfg in cands:
+        got = from_dev(kernels.matmul_int8_ex(0, to_dev(a), to_dev(wq), to_dev(s), config=cfg))
+        assert np.array_equal(got, want), cfg
+
+
+# ------------------------------------------------------------------ naive goldens vs the oracle
+
+def _naive_matmul(epi, a, b, bias=None, r=None):
+    M, Kd = a.shape
+    N = b.shape[1]
+    out = _empty_bf16((M, N))
+    _lib.check(_lib.load().pk_naive_matmul(epi, _ptr(a), _ptr(b), _ptr(out), _ptr(bias), _ptr(r), M, N, Kd,
+                                           _stream()), "pk_naive_matmul")
+    return out
+
+
+def test_naive_matmul_matches_oracle_bit_exact(gpu, oracle):
+    M, N, Kd = 67, 130, 259
+    a = synth.normal_bf16((M, Kd), 71)
+    b = synth.normal_bf16((Kd, N), 72, 1.0 / math.sqrt(Kd))
+    bias = synth.normal_bf16((N,), 73, 0.5)
+    r = synth.normal_bf16((M, N), 74)
+    da, db, dbias, dr = to_dev(a), to_dev(b), to_dev(bias), to_dev(r)
+    assert np.array_equal(from_dev(_naive_matmul(0, da, db)), oracle.matmul(a, b))
+    assert np.array_equal(from_dev(_naive_matmul(2, da, db, dbias, dr)),
+                          oracle.fused_matmul_bias_residual(a, b, bias, r))
+    # GELU: device erf(double) vs glibc erf may differ in the last double bit,
+    # which almost never moves the bf16 result
+    got = from_dev(_naive_matmul(1, da, db, dbias))
+    want = oracle.fused_matmul_bias_gelu(a, b, bias)
+    rep = mt.report(got, want)
+    assert rep.bit_exact >= 0.999 and rep.max_ulp <= 1, rep
+
+
+def test_naive_int8_rmsnorm_softmax_attention_match_oracle(gpu, oracle):
+    lib = _lib.load()
+    st = _stream()
+    # int8
+    M, N, Kd = 9, 96, 320
+    a = synth.normal_bf16((M, Kd), 75)
+    w = synth.normal_bf16((Kd, N), 76, 1.0 / math.sqrt(Kd))
+    wq, s = oracle.quantize_per_channel(w)
+    out = _empty_bf16((M, N))
+    _lib.check(lib.pk_naive_matmul_int8(0, _ptr(to_dev(a)), _ptr(to_dev(wq)), _ptr(to_dev(s)), _ptr(out), None,
+                                        M, N, Kd, st), "naive int8")
+    assert np.array_equal(from_dev(out), oracle.matmul_int8(a, wq, s))
+    # residual rmsnorm
+    rows, cols = 37, 1000
+    x, r = synth.normal_bf16((rows, cols), 77), synth.normal_bf16((rows, cols), 78)
+    g = synth.normal_bf16((cols,), 79, 0.1, 1.0)
+    out = _empty_bf16((rows, cols))
+    _lib.check(lib.pk_naive_rmsnorm(_ptr(to_dev(x)), _ptr(to_dev(r)), _ptr(to_dev(g)), _ptr(out), rows, cols,
+                                    1e-6, st), "naive rmsnorm")
+    assert np.array_equal(from_dev(out), oracle.residual_rmsnorm(x, r, g, 1e-6))
+    # masked softmax (device expf vs host expf: last-bit differences allowed)
+    lg = synth.normal_f32((rows, cols), 80, 2.0)
+    mk = synth.mask_bf16((rows, cols), 81, 0.1)
+    out = _empty_bf16((rows, cols))
+    _lib.check(lib.pk_naive_softmax_mask(_ptr(to_dev(lg)), _ptr(to_dev(mk)), _ptr(out), rows, cols, st), "naive sm")
+    rep = mt.report(from_dev(out), oracle.softmax_mask(lg, mk))
+    assert rep.bit_exact >= 0.99 and rep.max_ulp <= 1, rep
+    # causal attention with S_kv > S_q
+    BH, Sq, Skv, D = 3, 40, 72, 64
+    q = synth.normal_bf16((1, BH, Sq, D), 82)
+    k = synth.normal_bf16((1, BH, Skv, D), 83)
+    v = synth.normal_bf16((1, BH, Skv, D), 84)
+    out = _empty_bf16((1, BH, Sq, D))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    _lib.check(lib.pk_naive_attention(_ptr(to_dev(q)), _ptr(to_dev(k)), _ptr(to_dev(v)), _ptr(out), BH, Sq, Skv, Skv,
+                                      D, scale, 1, st), "naive attention")
+    rep = mt.report(from_dev(out), oracle.attention_prefill(q, k, v, scale, True))
+    assert rep.bit_exact >= 0.99 and rep.max_ulp <= 1, rep
+
+
+def test_device_metrics_match_host_metrics(gpu):
+    got = synth.normal_bf16((1000, 333), 85)
+    want = synth.f32_to_bf16(f32(got) * np.float32(1.01) + np.float32(0.003))
+    out = (C.c_double * 4)()
+    _lib.check(_lib.load().pk_compare_bf16(_ptr(to_dev(got)), _ptr(to_dev(want)), got.size, out, _stream()),
+               "pk_compare_bf16")
+    rep = mt.report(got, want)
+    assert abs(out[0] - rep.cosine) < 1e-12 and abs(out[2] - rep.pcc) < 1e-12
+    assert abs(out[1] - rep.max_rel_err) <= 1e-12 * max(1.0, rep.max_rel_err)
+    assert abs(out[3] - rep.bit_exact) < 1e-12
+    same = to_dev(got)
+    _lib.check(_lib.load().pk_compare_bf16(_ptr(same), _ptr(same), got.size, out, _stream()), "same")
+    assert list(out) == [1.0, 0.0, 1.0, 1.0]
+    bad = got.copy()
+    bad[5, 5] = 0x7FC0  # NaN fails every metric
+    _lib.check(_lib.load().pk_compare_bf16(_ptr(to_dev(bad)), _ptr(to_dev(got)), got.size, out, _stream()), "nan")
+    assert math.isnan(out[0]) and math.isnan(out[1]) and math.isnan(out[2])
+
+
+# ------------------------------------------------------------------ autotuner
+
+SMALL = [
+    ("matmul", 256, 512, 256),
+    ("fused_matmul_bias_gelu", 512, 512, 512),
+    ("fused_matmul_bias_residual", 256, 256, 1024),
+    ("matmul_int8_gelu", 16, 1024, 2048),
+    ("matmul_int8_residual", 32, 512, 1024),
+    ("fused_rmsnorm_matmul", 64, 512, 768),
+    ("fused_residual_rmsnorm", 64, 4096, 0),
+    ("fused_softmax_mask", 64, 4096, 0),
+    ("fused_kv_append_attention", 128, 384, 128),
+]
+
+
+@pytest.mark.parametrize("op,M,N,Kd", SMALL)
+def test_autotune_small_shapes(gpu, op, M, N, Kd):
+    _say(f"autotune {op} {M},{N},{Kd}")
+    res = rt.autotune(op, M, N, Kd, iters=3, warmup=1, max_variants=6, rotate_bytes=0, batch_heads=4)
+    e = res["entry"]
+    assert e["gpu"] == "gfx950" and e["op"] == op and e["scored_by"] == "measure"
+    assert e["validated"], res
+    assert e["best"] in rt.candidates(op, M, N, Kd)
+    assert e["time_ms"] > 0
+    assert e["correctness"]["cosine"] >= 0.999 and e["correctness"]["pcc"] >= 0.99
+    for v in res["variants"]:
+        assert (v["time_ms"] is not None) == v["validated"]
+    fastest = min(v["time_ms"] for v in res["variants"] if v["validated"])
+    assert e["time_ms"] == fastest
+    # the library's default configuration is swept first
+    assert res["variants"][0]["config"] == rt.default_config(op, M, N, Kd)
+
+
+def test_autotune_gate_runs_before_timing(gpu):
+    """With a ceiling no variant can meet every variant is rejected and none
+    is timed; the entry is recorded as not validated."""
+    res = rt.autotune("matmul_int8", 16, 512, 1024, iters=2, warmup=1, rel_ceiling=-1.0, rotate_bytes=0)
+    assert not res["entry"]["validated"] and res["entry"]["time_ms"] is None
+    assert res["variants"] and all(not v["validated"] and v["time_ms"] is None for v in res["variants"])
+    cache = rt.KernelCache()
+    cache.put(res["entry"])
+    with pytest.raises(rt.RuntimeError_) as ei:
+        rt.Runtime(cache).resolve("matmul_int8", 16, 512, 1024)
+    assert "not validated" in ei.value.message
+
+
+# ------------------------------------------------------------------ detect -> select -> serve
+
+def test_runtime_serves_tuned_int8_entry(gpu, oracle):
+    from polykernel_amd import kernels
+
+    M, N, Kd = 16, 1024, 2048
+    res = rt.autotune("matmul_int8_residual", M, N, Kd, iters=3, warmup=1, max_variants=8, rotate_bytes=0)
+    assert res["entry"]["validated"]
+    cache = rt.KernelCache()
+    cache.put(res["entry"])
+    runtime = rt.Runtime(cache)  # the HIP detector: this box's gfx950
+    a = int_bf16((M, Kd), 90)
+    wq = np.random.default_rng(91).integers(-127, 128, size=(Kd, N)).astype(np.int8)
+    s = (2.0 ** np.random.default_rng(92).integers(-8, -2, size=N)).astype(np.float32)
+    r = int_bf16((M, N), 93)
+    da, dw, ds, dr = to_dev(a), to_dev(wq), to_dev(s), to_dev(r)
+    out = _empty_bf16((M, N))
+    io = rt.MatmulInt8IO(A=_ptr(da), Wq=_ptr(dw), scale=_ptr(ds), C=_ptr(out), residual=_ptr(dr),
+                         M=M, N=N, K=Kd, workspace=None, workspace_bytes=0, stream=_stream())
+    runtime.run("matmul_int8_residual", M, N, Kd, io)
+    served = from_dev(out)
+    direct = from_dev(kernels.matmul_int8_ex(2, da, dw, ds, residual=dr, config=res["entry"]["best"]))
+    assert np.array_equal(served, direct)
+    want = oracle.add(oracle.matmul_int8(a, wq, s), r)
+    assert np.array_equal(served, want)
+
+
+def test_runtime_serves_gemm_and_refuses_mismatch(gpu, oracle):
+    M, N, Kd = 256, 512, 512
+    res = rt.autotune("fused_matmul_bias_gelu", M, N, Kd, iters=2, warmup=1, rotate_bytes=0)
+    cache = rt.KernelCache()
+    cache.put(res["entry"])
+    runtime = rt.Runtime(cache)
+    a, b = int_bf16((M, Kd), 94), int_bf16((Kd, N), 95)
+    bias = synth.normal_bf16((N,), 96, 0.5)
+    da, db, dbias = to_dev(a), to_dev(b), to_dev(bias)
+    out = _empty_bf16((M, N))
+    io = rt.MatmulIO(A=_ptr(da), B=_ptr(db), C=_ptr(out), bias=_ptr(dbias), residual=None, M=M, N=N, K=Kd,
+                     stream=_stream())
+    runtime.run("fused_matmul_bias_gelu", M, N, Kd, io)
+    assert np.array_equal(from_dev(out), oracle.fused_matmul_bias_gelu(a, b, bias))
+    with pytest.raises(rt.RuntimeError_) as ei:
+        runtime.run("fused_matmul_bias_gelu", M, N, Kd + 64, io)
+    assert "no tuned kernel" in ei.value.message
