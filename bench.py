@@ -6,9 +6,12 @@
 A step is one pass of the MLP block over the config-2 batch (BASELINE.json
 configs[1]): RMSNorm(x, gamma) -> MatMul W1 [4096,16384] + b1 -> GELU(erf) ->
 MatMul W2 [16384,4096] + b2 -> + x, x bf16 [4096,4096], synthetic seeded inputs
-resident in HBM before timing.  The step issues the same three C-ABI launches
-launch_mlp_block makes (rmsnorm, GEMM+bias+GELU, GEMM+bias+residual), with HIP
-events around the dominant GEMM launch on the stream it runs on.
+resident in HBM before timing.  The step issues the same three launches
+launch_mlp_block makes (rmsnorm, GEMM+bias+GELU, GEMM+bias+residual); the two
+GEMMs are served by the runtime (detect -> select -> serve) from the committed
+gfx950 tuning cache (polykernel_amd/tuning/gfx950.json, written by the
+correctness-gated autotuner), with HIP events around the dominant GEMM launch
+on the stream it runs on.
 
 value = 2^40 algorithmic FLOP per step / wall time per step (TFLOP/s).
 The other BASELINE configs (attention prefill, residual+RMSNorm, masked
@@ -63,7 +66,13 @@ def bench_mlp(steps: int, warmup: int):
     from polykernel_amd import _lib, synth
     from polykernel_amd._lib import check
 
+    from polykernel_amd import runtime as prt
+
     lib = _lib.load()
+    served = prt.default_runtime()
+    entry1 = served.resolve("fused_matmul_bias_gelu", M, F, D)
+    entry2 = served.resolve("fused_matmul_bias_residual", M, D, F)
+    log(f"served configs: gemm1 {entry1['best']}, gemm2 {entry2['best']}")
     t0 = time.time()
     x = synth.normal_bf16((M, D), 1, seed=SEED)
     g = synth.normal_bf16((D,), 2, 0.1, 1.0, seed=SEED)
@@ -79,17 +88,20 @@ def bench_mlp(steps: int, warmup: int):
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
+    io1 = prt.MatmulIO(A=a.data_ptr(), B=tw1.data_ptr(), C=h.data_ptr(), bias=tb1.data_ptr(), residual=None,
+                       M=M, N=F, K=D, stream=sp)
+    io2 = prt.MatmulIO(A=h.data_ptr(), B=tw2.data_ptr(), C=y.data_ptr(), bias=tb2.data_ptr(),
+                       residual=tx.data_ptr(), M=M, N=D, K=F, stream=sp)
+
     def step(ev=None):
         check(lib.launch_rmsnorm(tx.data_ptr(), tg.data_ptr(), a.data_ptr(), M, D, 1e-6, sp), "rmsnorm")
         if ev is not None:
             ev[0].record(stream)
-        check(lib.pk_gemm_ex(1, a.data_ptr(), tw1.data_ptr(), h.data_ptr(), tb1.data_ptr(), None,
-                             M, F, D, -1, sp), "gemm1")
+        served.run("fused_matmul_bias_gelu", M, F, D, io1)
         if ev is not None:
             ev[1].record(stream)
             ev[2].record(stream)
-        check(lib.pk_gemm_ex(2, h.data_ptr(), tw2.data_ptr(), y.data_ptr(), tb2.data_ptr(), tx.data_ptr(),
-                             M, D, F, -1, sp), "gemm2")
+        served.run("fused_matmul_bias_residual", M, D, F, io2)
         if ev is not None:
             ev[3].record(stream)
 
@@ -106,7 +118,8 @@ def bench_mlp(steps: int, warmup: int):
     g1 = [e[0].elapsed_time(e[1]) for e in evs]
     g2 = [e[2].elapsed_time(e[3]) for e in evs]
 
-    # the product entry point on the same buffers (equal work; reported for reference)
+    # the library's plain entry point (its built-in configs) on the same
+    # buffers: equal work, reported beside the served path
     ws = torch.empty(lib.pk_mlp_block_workspace_size(M, D, F), dtype=torch.uint8, device="cuda")
     e0, e1 = event_pair()
     e0.record(stream)
@@ -118,7 +131,7 @@ def bench_mlp(steps: int, warmup: int):
     torch.cuda.synchronize()
     entry_ms = e0.elapsed_time(e1) / 3
     inputs = dict(x=x, g=g, w1=w1, b1=b1, w2=w2, b2=b2)
-    return elapsed, g1, g2, entry_ms, inputs
+    return elapsed, g1, g2, entry_ms, inputs, (entry1, entry2)
 
 
 def bench_extra(reps: int = 20):
@@ -127,6 +140,7 @@ def bench_extra(reps: int = 20):
     import torch
 
     from polykernel_amd import _lib, kernels, synth
+    from polykernel_amd import runtime as prt
     from polykernel_amd._lib import check
 
     lib = _lib.load()
@@ -220,11 +234,33 @@ def bench_extra(reps: int = 20):
             xd.data_ptr(), a.data_ptr(), s1.data_ptr(), b.data_ptr(), s2.data_ptr(), od.data_ptr(),
             Md, dd, Fd, ws.data_ptr(), ws.numel(), sp), "cfg5")
 
-    ms = timeit(decode)
+    ms_entry = timeit(decode)
+    # the same chain served by the runtime with the tuned configs
+    served = prt.default_runtime()
+    hd = torch.empty(Md, Fd, dtype=torch.bfloat16, device="cuda")
+    ios = []
+    for a, b in wsets:
+        ios.append((prt.MatmulInt8IO(A=xd.data_ptr(), Wq=a.data_ptr(), scale=s1.data_ptr(), C=hd.data_ptr(),
+                                     residual=None, M=Md, N=Fd, K=dd, workspace=None, workspace_bytes=0,
+                                     stream=sp),
+                    prt.MatmulInt8IO(A=hd.data_ptr(), Wq=b.data_ptr(), scale=s2.data_ptr(), C=od.data_ptr(),
+                                     residual=xd.data_ptr(), M=Md, N=dd, K=Fd, workspace=None,
+                                     workspace_bytes=0, stream=sp)))
+
+    def decode_served():
+        i1, i2 = ios[turn[0] % 2]
+        turn[0] += 1
+        served.run("matmul_int8_gelu", Md, Fd, dd, i1)
+        served.run("matmul_int8_residual", Md, dd, Fd, i2)
+
+    ms = timeit(decode_served)
     gbs = 470433792 / (ms * 1e-3) / 1e9
-    out["int8_decode_mlp_cfg5"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
-                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-                                   "note": "2 weight copies in turn (no MALL reuse)"}
+    out["int8_decode_mlp_cfg5"] = {
+        "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+        "launch_decode_mlp_int8_us": round(ms_entry * 1e3, 2),
+        "served_configs": [served.resolve("matmul_int8_gelu", Md, Fd, dd)["best"],
+                           served.resolve("matmul_int8_residual", Md, dd, Fd)["best"]],
+        "note": "runtime-served tuned configs; 2 weight copies in turn (no MALL reuse)"}
     return out
 
 
@@ -311,7 +347,7 @@ def main() -> int:
 
     _lib.load()
     log(f"device: {torch.cuda.get_device_name(0)}")
-    elapsed, g1, g2, entry_ms, inputs = bench_mlp(args.steps, args.warmup)
+    elapsed, g1, g2, entry_ms, inputs, entries = bench_mlp(args.steps, args.warmup)
     ms_step = elapsed / args.steps * 1e3
     value = MLP_FLOP / (ms_step * 1e-3) / 1e12
     g1_ms = sum(g1) / len(g1)
@@ -326,6 +362,7 @@ def main() -> int:
         "gemm1_bias_gelu_ms": round(g1_ms, 4), "gemm2_bias_residual_ms": round(g2_ms, 4),
         "gemm2_tflops": round(GEMM_FLOP / (g2_ms * 1e-3) / 1e12, 1),
         "launch_mlp_block_ms": round(entry_ms, 4),
+        "served_configs": [entries[0]["best"], entries[1]["best"]],
         "frac_mfma_block": round(value / PEAK_BF16_TFLOPS, 4)}
     cpu = None
     if not args.no_cpu:
@@ -350,7 +387,8 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": read_traffic(),
-                     "kernel": "gemm_dma_kernel<EPI_BIAS_GELU,5> (GEMM1: x@W1+b1->GELU, 2^39 FLOP/launch)"},
+                     "kernel": f"gemm_dma_kernel<EPI_BIAS_GELU,{entries[0]['best']['shared_memory_stages']}> "
+                               "(GEMM1: x@W1+b1->GELU, 2^39 FLOP/launch)"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -216,8 +216,9 @@ class PK_API HipEventTimer {
 struct AutotuneOptions {
   int warmup = 3;
   int iters = 20;
-  // Weight-stream ops are timed over rotating copies of their inputs whose
-  // total reaches this many bytes, so the 256 MiB MALL does not serve them.
+  // HBM-bound ops (int8, row-wise, softmax) are timed over rotating copies of
+  // their inputs whose total reaches this many bytes (at most 4 copies), so
+  // the 256 MiB MALL does not serve them; MFMA-bound ops use one copy.
   std::size_t rotate_bytes = std::size_t(600) << 20;
   std::optional<double> rel_ceiling;   // default RelCeiling(op, K)
   std::optional<std::size_t> max_variants;  // sweep only the first N candidates
@@ -309,9 +310,13 @@ class PK_API DeviceDetector {
 // "gfx950:sramecc+:xnack-" -> "gfx950"; "" when no gfx<digit> token.
 PK_API std::string ParseGcnArchName(std::string_view gcn_arch_name);
 
+// hipGetDeviceProperties of `ordinal`, queried once per process and ordinal.
 class PK_API HipDeviceDetector final : public DeviceDetector {
  public:
   std::optional<DeviceInfo> Detect(int ordinal = 0) const override;
+
+ private:
+  static std::optional<DeviceInfo> Query(int ordinal);
 };
 
 class PK_API FixedArchDetector final : public DeviceDetector {

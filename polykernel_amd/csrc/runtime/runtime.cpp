@@ -7,6 +7,9 @@
 // xnack-") to its bare token like lib/Runtime/DeviceDetect.cpp:28-50.
 #include <hip/hip_runtime_api.h>
 
+#include <map>
+#include <mutex>
+
 #include "../../../include/polykernel_amd_runtime.hpp"
 
 namespace pk::runtime {
@@ -20,7 +23,23 @@ std::string ParseGcnArchName(std::string_view s) {
   return std::string(s.substr(pos, end - pos));
 }
 
+// Device properties do not change while a process runs, and Runtime::Run
+// detects on every call: the first answer per ordinal is kept.
 std::optional<DeviceInfo> HipDeviceDetector::Detect(int ordinal) const {
+  static std::mutex mu;
+  static std::map<int, std::optional<DeviceInfo>> seen;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = seen.find(ordinal);
+    if (it != seen.end()) return it->second;
+  }
+  std::optional<DeviceInfo> info = Query(ordinal);
+  std::lock_guard<std::mutex> lock(mu);
+  seen.emplace(ordinal, info);
+  return info;
+}
+
+std::optional<DeviceInfo> HipDeviceDetector::Query(int ordinal) {
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || ordinal < 0 || ordinal >= count) {
     (void)hipGetLastError();

@@ -229,3 +229,21 @@ class Runtime:
     def run(self, op: str, m: int, n: int, k: int, io: C.Structure, dtype: Optional[str] = None) -> None:
         _call(f"Run {op}", self._lib.pk_runtime_run(self._h, _s(op), m, n, k, _s(dtype or op_dtype(op)),
                                                     C.byref(io)))
+
+
+# ---- the committed gfx950 tuning cache ----------------------------------------------
+
+TUNING_FILE = _lib._PKG / "tuning" / "gfx950.json"
+
+
+def default_cache() -> KernelCache:
+    """A KernelCache holding the committed gfx950 entries (polykernel_amd/tuning/gfx950.json,
+    written by `python -m polykernel_amd.autotune --baseline`)."""
+    cache = KernelCache()
+    cache.load_tuning_cache(TUNING_FILE.read_text())
+    return cache
+
+
+def default_runtime() -> Runtime:
+    """Runtime over default_cache() with the HIP device detector."""
+    return Runtime(default_cache())
