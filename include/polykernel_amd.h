@@ -232,6 +232,13 @@ PK_API int pk_gemm_config_ex(int epi, const uint16_t *A, const uint16_t *B, uint
                              const uint16_t *bias, const uint16_t *R, int M, int N, int K,
                              const pk_config *cfg, void *stream);
 
+/* ---- code-object support ----------------------------------------------------- */
+/* What a host needs to launch the emitted code objects: the device GELU table
+ * of the current device (built on first use) and the library-owned
+ * per-device workspace (grown on demand, kept until the process ends). */
+PK_API int pk_gelu_table(const uint16_t **table);
+PK_API int pk_library_workspace(size_t bytes, void **ptr);
+
 /* ---- naive device goldens (the autotuner's correctness gate) --------------- */
 /* Straightforward one-thread-per-output kernels that restate the reference
  * semantics in their own sequential order (fp32 multiply then add, no

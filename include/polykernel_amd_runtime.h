@@ -136,12 +136,27 @@ typedef struct pk_runtime pk_runtime;
  * fixed detector reporting that arch (for tests). */
 PK_API pk_runtime *pk_runtime_create(const pk_kernel_cache *cache, const char *fixed_arch);
 PK_API void pk_runtime_destroy(pk_runtime *rt);
+/* As pk_runtime_create; with PK_RUNTIME_CODE_OBJECTS in `flags` the int8
+ * ops are served from the code objects the cache holds for their entries
+ * (pk_emit_code_object) instead of the linked kernels. */
+#define PK_RUNTIME_CODE_OBJECTS 1
+PK_API pk_runtime *pk_runtime_create_ex(const pk_kernel_cache *cache, const char *fixed_arch, int flags);
 /* detect + select; the entry -> pk_last_text(). */
 PK_API int pk_runtime_resolve(pk_runtime *rt, const char *op, long long M, long long N, long long K,
                               const char *dtype);
 /* detect + select + serve; `io` points at the op's pk_*_io block. */
 PK_API int pk_runtime_run(pk_runtime *rt, const char *op, long long M, long long N, long long K, const char *dtype,
                           void *io);
+
+/* ---- emitter ------------------------------------------------------------------ */
+/* The gfx950 HIP source of a tuned entry (JSON, schema entry form) ->
+ * pk_last_text(); only the int8 ops are emitted. */
+PK_API int pk_emit_source(const char *entry_json);
+/* Emit + compile (hipcc --genco, child process) the entry's code object into
+ * out_dir, then record the entry and the object's path and FNV-1a hash in
+ * `cache`.  csrc_dir: the directory holding int8_stream.hpp. */
+PK_API int pk_emit_code_object(pk_kernel_cache *cache, const char *entry_json, const char *csrc_dir,
+                               const char *out_dir);
 
 /* ---- autotuner ------------------------------------------------------------ */
 /* Sweep (op, shape) on the current device.  options_json may be NULL or an

@@ -368,6 +368,13 @@ using KvAppendAttentionIO = pk_kv_append_attention_io;
 // config is one the kernels implement, then launches through the C-ABI.
 PK_API void RegisterBuiltinLaunchers(Runtime &runtime);
 
+// Serve matmul_int8, matmul_int8_gelu and matmul_int8_residual from the code
+// objects `cache` holds for their entries (codegen::EmitCodeObject): the
+// object is loaded once (hash-checked) and launched with
+// hipModuleLaunchKernel.  An entry without a cached code object is an error.
+// `cache` must outlive the runtime.
+PK_API void RegisterCodeObjectLaunchers(Runtime &runtime, const KernelCache &cache);
+
 // ---- code objects -------------------------------------------------------------
 // A code object loaded with hipModuleLoad (the binary half of a cache entry).
 class PK_API CodeObject {
@@ -391,3 +398,21 @@ class PK_API CodeObject {
 };
 
 }  // namespace pk::runtime
+
+namespace pk::codegen {
+
+// The gfx950 HIP source of a tuned int8 entry: the streaming kernel's
+// template instantiated at the entry's config behind extern "C" entry points
+// pk_int8_stream / pk_int8_reduce.  Other ops are served by the linked
+// kernels and are refused.
+PK_API bool EmitSource(const autotune::CacheEntry &entry, std::string &source, std::string &error);
+// hipcc --genco for gfx950 (the library's flags) in a child process; the
+// kernel headers are found under csrc_dir.
+PK_API bool CompileCodeObject(const std::string &source_path, const std::string &csrc_dir,
+                              const std::string &out_path, std::string &error);
+// Emit + compile into out_dir, then record the entry and its code object
+// (absolute path, FNV-1a hash) in `cache`.
+PK_API bool EmitCodeObject(runtime::KernelCache &cache, const autotune::CacheEntry &entry,
+                           const std::string &csrc_dir, const std::string &out_dir, std::string &error);
+
+}  // namespace pk::codegen

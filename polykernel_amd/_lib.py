@@ -114,6 +114,11 @@ SIGNATURES = {
     "pk_select_best_validated": (I, [C.POINTER(I), C.POINTER(D), I]),
     "pk_config_candidates": (I, [C.c_char_p, LL, LL, LL, C.c_char_p]),
     "pk_runtime_create": (P, [P, C.c_char_p]),
+    "pk_runtime_create_ex": (P, [P, C.c_char_p, I]),
+    "pk_emit_source": (I, [C.c_char_p]),
+    "pk_emit_code_object": (I, [P, C.c_char_p, C.c_char_p, C.c_char_p]),
+    "pk_gelu_table": (I, [C.POINTER(P)]),
+    "pk_library_workspace": (I, [SZ, C.POINTER(P)]),
     "pk_runtime_destroy": (None, [P]),
     "pk_runtime_resolve": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p]),
     "pk_runtime_run": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p, P]),

@@ -173,6 +173,22 @@ const char *pk_version(void) { return "polykernel_amd 0.1.0 gfx950"; }
 
 const char *pk_last_error(void) { return g_err; }
 
+int pk_gelu_table(const uint16_t **table) {
+  if (!table) {
+    set_error("pk_gelu_table: null argument");
+    return PK_ERR_INVALID_ARG;
+  }
+  return gelu_table(table);
+}
+
+int pk_library_workspace(size_t bytes, void **ptr) {
+  if (!ptr) {
+    set_error("pk_library_workspace: null argument");
+    return PK_ERR_INVALID_ARG;
+  }
+  return library_workspace(bytes, ptr);
+}
+
 int pk_init(void) {
   const uint16_t *t = nullptr;
   return gelu_table(&t);

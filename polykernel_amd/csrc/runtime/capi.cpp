@@ -152,7 +152,7 @@ PK_API int pk_config_candidates(const char *op, long long M, long long N, long l
   return Text(pk::json::Serialize(pk::json::Value(std::move(arr))));
 }
 
-PK_API pk_runtime *pk_runtime_create(const pk_kernel_cache *c, const char *fixed_arch) {
+PK_API pk_runtime *pk_runtime_create_ex(const pk_kernel_cache *c, const char *fixed_arch, int flags) {
   if (!c) {
     pk::set_error("pk_runtime_create: null cache");
     return nullptr;
@@ -161,8 +161,49 @@ PK_API pk_runtime *pk_runtime_create(const pk_kernel_cache *c, const char *fixed
   if (fixed_arch) d = std::make_unique<pk::runtime::FixedArchDetector>(fixed_arch);
   else d = std::make_unique<pk::runtime::HipDeviceDetector>();
   auto *rt = new (std::nothrow) pk_runtime(std::move(d), c->cache);
-  if (rt) pk::runtime::RegisterBuiltinLaunchers(rt->rt);
+  if (!rt) return nullptr;
+  pk::runtime::RegisterBuiltinLaunchers(rt->rt);
+  if (flags & PK_RUNTIME_CODE_OBJECTS) pk::runtime::RegisterCodeObjectLaunchers(rt->rt, c->cache);
   return rt;
+}
+
+PK_API pk_runtime *pk_runtime_create(const pk_kernel_cache *c, const char *fixed_arch) {
+  return pk_runtime_create_ex(c, fixed_arch, 0);
+}
+
+namespace {
+bool ParseEntry(const char *entry_json, CacheEntry &e, std::string &error) {
+  if (!entry_json) {
+    error = "null entry";
+    return false;
+  }
+  pk::autotune::TuningCacheParseResult p =
+      pk::autotune::ParseTuningCache(std::string("{\"version\":1,\"entries\":[") + entry_json + "]}");
+  if (!p.ok()) {
+    error = p.error;
+    return false;
+  }
+  e = p.cache->entries.at(0);
+  return true;
+}
+}  // namespace
+
+PK_API int pk_emit_source(const char *entry_json) {
+  CacheEntry e;
+  std::string err, src;
+  if (!ParseEntry(entry_json, e, err)) return Fail(PK_ERR_INVALID_ARG, "pk_emit_source: " + err);
+  if (!pk::codegen::EmitSource(e, src, err)) return Fail(PK_ERR_UNSUPPORTED, err);
+  return Text(src);
+}
+
+PK_API int pk_emit_code_object(pk_kernel_cache *c, const char *entry_json, const char *csrc_dir,
+                               const char *out_dir) {
+  if (!c || !csrc_dir || !out_dir) return Fail(PK_ERR_INVALID_ARG, "pk_emit_code_object: null argument");
+  CacheEntry e;
+  std::string err;
+  if (!ParseEntry(entry_json, e, err)) return Fail(PK_ERR_INVALID_ARG, "pk_emit_code_object: " + err);
+  if (!pk::codegen::EmitCodeObject(c->cache, e, csrc_dir, out_dir, err)) return Fail(PK_ERR_UNSUPPORTED, err);
+  return PK_OK;
 }
 
 PK_API void pk_runtime_destroy(pk_runtime *rt) { delete rt; }

@@ -1,0 +1,182 @@
+// codegen.cpp -- the gfx950 emitter: a tuned cache entry becomes a standalone
+// code object (.hsaco) that the runtime loads with hipModuleLoad.
+//
+// The reference lowers its IR ops to generic HIP/CUDA source
+// (lib/Codegen/LowerToHip.cpp) and compiles per-op shared libraries.  Here the
+// kernels already exist as templates written for gfx950; emitting a tuned
+// variant means instantiating the template at the entry's configuration
+// behind extern "C" entry points with fixed names, and compiling that one
+// translation unit for gfx950 with hipcc --genco.  The code object's FNV-1a
+// hash goes into the KernelCache beside the entry, so a code object that
+// changes on disk is refused (CodeObject::Load) and dropped
+// (KernelCache::InvalidateStale).
+//
+// Emitted entry points (matmul_int8, matmul_int8_gelu, matmul_int8_residual):
+//   pk_int8_stream(pk_i8s_args)   grid (slices * splits, m-blocks), 64 * num_warps threads
+//   pk_int8_reduce(pk_i8s_args)   the split reduction, 256 threads
+#include <fcntl.h>
+#include <spawn.h>
+#include <sys/wait.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <sstream>
+
+#include "internal.hpp"
+
+extern char **environ;
+
+namespace pk::codegen {
+
+using autotune::CacheEntry;
+using autotune::Config;
+
+namespace {
+
+int Int8Epilogue(const std::string &op) {
+  if (op == "matmul_int8") return 0;
+  if (op == "matmul_int8_gelu") return 1;
+  if (op == "matmul_int8_residual") return 2;
+  return -1;
+}
+
+std::string Hipcc() {
+  if (const char *p = std::getenv("HIPCC")) return p;
+  const char *rocm = std::getenv("ROCM_PATH");
+  return std::string(rocm ? rocm : "/opt/rocm") + "/bin/hipcc";
+}
+
+// Run argv[0] with argv as a child process; its output goes to `log`.
+bool RunChild(const std::vector<std::string> &argv, const std::string &log, std::string &error) {
+  std::vector<char *> args;
+  for (const std::string &a : argv) args.push_back(const_cast<char *>(a.c_str()));
+  args.push_back(nullptr);
+  posix_spawn_file_actions_t fa;
+  posix_spawn_file_actions_init(&fa);
+  posix_spawn_file_actions_addopen(&fa, 1, log.c_str(), O_WRONLY | O_CREAT | O_TRUNC, 0644);
+  posix_spawn_file_actions_adddup2(&fa, 1, 2);
+  pid_t pid = 0;
+  const int rc = posix_spawnp(&pid, args[0], &fa, nullptr, args.data(), environ);
+  posix_spawn_file_actions_destroy(&fa);
+  if (rc != 0) {
+    error = "cannot start " + argv[0] + ": " + std::strerror(rc);
+    return false;
+  }
+  int status = 0;
+  if (waitpid(pid, &status, 0) < 0 || !WIFEXITED(status) || WEXITSTATUS(status) != 0) {
+    std::ifstream in(log);
+    std::stringstream ss;
+    ss << in.rdbuf();
+    std::string out = ss.str();
+    if (out.size() > 4000) out = out.substr(out.size() - 4000);
+    error = argv[0] + " failed (status " + std::to_string(status) + "):\n" + out;
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
+  const int epi = Int8Epilogue(e.op);
+  if (epi < 0) {
+    error = "the emitter instantiates the int8 ops (matmul_int8, matmul_int8_gelu, matmul_int8_residual); " +
+            e.op + " is served by the linked kernels";
+    return false;
+  }
+  const std::vector<Config> cands = autotune::ConfigSpace::Candidates(e.op, e.shape);
+  if (std::find(cands.begin(), cands.end(), e.best) == cands.end()) {
+    error = "config {" + autotune::ToString(e.best) + "} is not one the gfx950 kernels implement for " +
+            runtime::FormatKey(e.gpu, e.op, e.shape);
+    return false;
+  }
+  if (e.gpu != "gfx950") {
+    error = "the emitter targets gfx950, not " + e.gpu;
+    return false;
+  }
+  const Config &c = e.best;
+  const int nt = c.block_n / (16 * c.num_warps), mt = c.block_m / 16;
+  std::ostringstream s;
+  s << "// Emitted by the polykernel_amd gfx950 emitter for " << runtime::FormatKey(e.gpu, e.op, e.shape) << "\n"
+    << "// config: " << autotune::ToString(c) << "\n"
+    << "#include \"int8_stream.hpp\"\n\n"
+    << "extern \"C\" __global__ __launch_bounds__(" << 64 * c.num_warps << ", 1) void pk_int8_stream(pk_i8s_args g) {\n"
+    << "  pk::i8s::stream_body<" << nt << ", " << mt << ", " << c.num_warps << ", " << c.shared_memory_stages << ", "
+    << epi << ">(g);\n}\n\n"
+    << "extern \"C\" __global__ __launch_bounds__(256) void pk_int8_reduce(pk_i8s_args g) {\n"
+    << "  pk::i8s::reduce8_body<" << epi << ">(g.partial, g.splits, g.M, g.N, g.scale, g.R, g.gelu_tab, g.C);\n}\n";
+  source = s.str();
+  return true;
+}
+
+bool CompileCodeObject(const std::string &source_path, const std::string &csrc_dir, const std::string &out_path,
+                       std::string &error) {
+  const std::vector<std::string> argv = {Hipcc(),
+                                         "--offload-arch=gfx950",
+                                         "--genco",
+                                         "--no-gpu-bundle-output",  // a plain ELF code object
+                                         "-O3",
+                                         "-std=c++17",
+                                         "-Xclang",
+                                         "-target-feature",
+                                         "-Xclang",
+                                         "-packed-fp32-ops",
+                                         "-mllvm",
+                                         "-pragma-unroll-threshold=1000000",
+                                         "-I",
+                                         csrc_dir,
+                                         "-I",
+                                         csrc_dir + "/../../include",
+                                         source_path,
+                                         "-o",
+                                         out_path};
+  if (!RunChild(argv, out_path + ".log", error)) return false;
+  std::ifstream in(out_path, std::ios::binary);
+  char magic[4] = {};
+  in.read(magic, 4);
+  if (!in || magic[0] != 0x7f || magic[1] != 'E' || magic[2] != 'L' || magic[3] != 'F') {
+    error = out_path + " is not an ELF code object";
+    return false;
+  }
+  return true;
+}
+
+bool EmitCodeObject(runtime::KernelCache &cache, const CacheEntry &e, const std::string &csrc_dir,
+                    const std::string &out_dir, std::string &error) {
+  std::string source;
+  if (!EmitSource(e, source, error)) return false;
+  std::error_code ec;
+  std::filesystem::create_directories(out_dir, ec);
+  if (ec) {
+    error = "cannot create " + out_dir + ": " + ec.message();
+    return false;
+  }
+  // one file per (op, shape, config): a re-tuned entry gets a new object
+  const Config &c = e.best;
+  std::ostringstream name;
+  name << e.op << "_M" << e.shape.m << "_N" << e.shape.n << "_K" << e.shape.k << "_" << c.block_m << "x" << c.block_n
+       << "x" << c.block_k << "_w" << c.num_warps << "_s" << c.shared_memory_stages;
+  const std::string base = std::filesystem::absolute(std::filesystem::path(out_dir) / name.str()).string();
+  {
+    std::ofstream out(base + ".hip");
+    out << source;
+    if (!out) {
+      error = "cannot write " + base + ".hip";
+      return false;
+    }
+  }
+  if (!CompileCodeObject(base + ".hip", csrc_dir, base + ".hsaco", error)) return false;
+  std::string hash;
+  if (!runtime::HashFile(base + ".hsaco", hash, error)) return false;
+  if (!cache.Put(e) || !cache.PutBinary(e.gpu, e.op, e.shape, runtime::CachedBinary{base + ".hsaco", hash})) {
+    error = "cannot record the code object of " + runtime::FormatKey(e.gpu, e.op, e.shape);
+    return false;
+  }
+  return true;
+}
+
+}  // namespace pk::codegen

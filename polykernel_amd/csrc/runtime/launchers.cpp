@@ -7,9 +7,15 @@
 // shape (a hand-edited or foreign cache entry is an error, never a silent
 // re-tune), then launches through the C-ABI with the entry's config.  The
 // reference's LaunchFn contract is lib/Runtime/Runtime.h:47-48.
+#include <hip/hip_runtime_api.h>
+
 #include <algorithm>
+#include <map>
+#include <memory>
+#include <mutex>
 
 #include "../../../include/polykernel_amd_runtime.hpp"
+#include "../int8_args.h"
 
 namespace pk::runtime {
 
@@ -69,7 +75,117 @@ LaunchFn Int8Launcher(int epi) {
   };
 }
 
+// Code objects loaded by the code-object launchers, keyed by path and hash.
+struct ModuleTable {
+  struct Loaded {
+    CodeObject module;
+    void *stream_fn = nullptr;
+    void *reduce_fn = nullptr;
+  };
+  const KernelCache &cache;
+  std::mutex mu;
+  std::map<std::string, std::unique_ptr<Loaded>> loaded;
+
+  explicit ModuleTable(const KernelCache &c) : cache(c) {}
+
+  Loaded *Get(const CachedBinary &bin, std::string &error) {
+    std::lock_guard<std::mutex> lock(mu);
+    const std::string key = bin.so_path + "#" + bin.kernel_hash;
+    auto it = loaded.find(key);
+    if (it != loaded.end()) return it->second.get();
+    auto l = std::make_unique<Loaded>();
+    if (!l->module.Load(bin, error)) return nullptr;
+    if (!(l->stream_fn = l->module.Function("pk_int8_stream", error))) return nullptr;
+    if (!(l->reduce_fn = l->module.Function("pk_int8_reduce", error))) return nullptr;
+    Loaded *raw = l.get();
+    loaded.emplace(key, std::move(l));
+    return raw;
+  }
+};
+
+bool Aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool ModuleLaunch(void *fn, unsigned gx, unsigned gy, unsigned threads, void *stream, pk_i8s_args &args,
+                  const char *what, std::string &error) {
+  void *params[] = {&args};
+  const hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), gx, gy, 1, threads, 1, 1, 0,
+                                             static_cast<hipStream_t>(stream), params, nullptr);
+  if (e != hipSuccess) {
+    error = std::string("hip launch failed for ") + what + ": " + hipGetErrorString(e);
+    (void)hipGetLastError();
+    return false;
+  }
+  return true;
+}
+
+// The launch geometry of an int8 config follows from its fields: column
+// slices of block_n, K splits of block_k rows (64-row steps), row blocks of
+// block_m; the streaming kernel and, with more than one split, the split
+// reduction (as int8_run launches them).
+LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
+  return [epi, table](const CacheEntry &e, void *io, std::string &error) {
+    MatmulInt8IO *p = Cast<MatmulInt8IO>(io, error);
+    if (!p || !CheckEntry(e, p->M, p->N, p->K, error)) return false;
+    const std::optional<CachedBinary> bin = table->cache.GetBinary(e.gpu, e.op, e.shape);
+    if (!bin) {
+      error = "no code object cached for " + FormatKey(e.gpu, e.op, e.shape) +
+              "; emit one (python -m polykernel_amd.emit)";
+      return false;
+    }
+    ModuleTable::Loaded *mod = table->Get(*bin, error);
+    if (!mod) return false;
+    if (!Aligned16(p->A) || !Aligned16(p->Wq) || !Aligned16(p->scale) || !Aligned16(p->C) ||
+        (epi == 2 && (!p->residual || !Aligned16(p->residual)))) {
+      error = "code-object int8 launch needs 16-byte aligned A, Wq, scale, C and residual";
+      return false;
+    }
+    const Config &c = e.best;
+    const int ksteps = p->K / 64;
+    const int split_steps = std::min(ksteps, c.block_k / 64);
+    const int splits = (ksteps + split_steps - 1) / split_steps;
+    const int slices = (p->N + c.block_n - 1) / c.block_n;
+    const int mblocks = (p->M + c.block_m - 1) / c.block_m;
+    void *ws = nullptr;
+    if (splits > 1) {
+      const size_t need = (size_t)splits * p->M * p->N * sizeof(float);
+      if (p->workspace) {
+        if (p->workspace_bytes < need || !Aligned16(p->workspace)) {
+          error = "workspace of " + std::to_string(need) + " aligned bytes required";
+          return false;
+        }
+        ws = p->workspace;
+      } else if (pk_library_workspace(need, &ws) != PK_OK) {
+        error = std::string("library workspace: ") + pk_last_error();
+        return false;
+      }
+    }
+    const uint16_t *tab = nullptr;
+    if (epi == 1 && pk_gelu_table(&tab) != PK_OK) {
+      error = std::string("GELU table: ") + pk_last_error();
+      return false;
+    }
+    pk_i8s_args a{p->A, p->Wq, p->scale, static_cast<float *>(ws), p->C, epi == 2 ? p->residual : nullptr, tab,
+                  p->M, p->N, p->K, splits, split_steps, slices * splits};
+    if (!ModuleLaunch(mod->stream_fn, (unsigned)(slices * splits), (unsigned)mblocks, 64u * c.num_warps, p->stream, a,
+                      "pk_int8_stream", error))
+      return false;
+    if (splits > 1) {
+      const long long groups = (long long)p->M * p->N / 8;
+      const unsigned blocks = (unsigned)std::min<long long>((groups + 255) / 256, 4096);
+      if (!ModuleLaunch(mod->reduce_fn, blocks, 1, 256, p->stream, a, "pk_int8_reduce", error)) return false;
+    }
+    return true;
+  };
+}
+
 }  // namespace
+
+void RegisterCodeObjectLaunchers(Runtime &rt, const KernelCache &cache) {
+  auto table = std::make_shared<ModuleTable>(cache);
+  rt.RegisterLauncher("matmul_int8", CodeObjectInt8Launcher(0, table));
+  rt.RegisterLauncher("matmul_int8_gelu", CodeObjectInt8Launcher(1, table));
+  rt.RegisterLauncher("matmul_int8_residual", CodeObjectInt8Launcher(2, table));
+}
 
 void RegisterBuiltinLaunchers(Runtime &rt) {
   rt.RegisterLauncher("matmul", GemmLauncher(0));

@@ -206,14 +206,19 @@ class KernelCache:
         return int(self._lib.pk_cache_invalidate_stale(self._h))
 
 
+CODE_OBJECTS = 1  # PK_RUNTIME_CODE_OBJECTS
+
+
 class Runtime:
     """detect -> select -> serve over a KernelCache, with every built-in
-    launcher registered.  fixed_arch=None detects the HIP device."""
+    launcher registered.  fixed_arch=None detects the HIP device.  With
+    code_objects=True the int8 ops are served from the code objects the cache
+    holds for their entries (emit_code_object), loaded with hipModuleLoad."""
 
-    def __init__(self, cache: KernelCache, fixed_arch: Optional[str] = None):
+    def __init__(self, cache: KernelCache, fixed_arch: Optional[str] = None, code_objects: bool = False):
         self._lib = _lib.load()
         self._cache = cache  # keep the cache alive for the runtime's lifetime
-        self._h = self._lib.pk_runtime_create(cache.handle, _s(fixed_arch))
+        self._h = self._lib.pk_runtime_create_ex(cache.handle, _s(fixed_arch), CODE_OBJECTS if code_objects else 0)
         if not self._h:
             raise RuntimeError_("pk_runtime_create", _lib.PK_ERR_INVALID_ARG, _lib.last_error())
 
@@ -229,6 +234,26 @@ class Runtime:
     def run(self, op: str, m: int, n: int, k: int, io: C.Structure, dtype: Optional[str] = None) -> None:
         _call(f"Run {op}", self._lib.pk_runtime_run(self._h, _s(op), m, n, k, _s(dtype or op_dtype(op)),
                                                     C.byref(io)))
+
+
+# ---- emitter --------------------------------------------------------------------------
+
+CSRC_DIR = _lib._PKG / "csrc"
+
+
+def emit_source(entry: dict) -> str:
+    """gfx950 HIP source instantiating a tuned int8 entry's kernel."""
+    _call("emit_source", _lib.load().pk_emit_source(_s(json.dumps(entry))))
+    return _lib.last_text()
+
+
+def emit_code_object(cache: KernelCache, entry: dict, out_dir) -> dict:
+    """Compile the entry's code object into out_dir (hipcc --genco, child
+    process) and record entry + object in `cache`; returns the binary record."""
+    _call("emit_code_object", _lib.load().pk_emit_code_object(cache.handle, _s(json.dumps(entry)),
+                                                              _s(str(CSRC_DIR)), _s(str(out_dir))))
+    sh = entry["shape"]
+    return cache.get_binary(entry["gpu"], entry["op"], sh["M"], sh["N"], sh["K"], sh["dtype"])
 
 
 # ---- the committed gfx950 tuning cache ----------------------------------------------
@@ -247,3 +272,15 @@ def default_cache() -> KernelCache:
 def default_runtime() -> Runtime:
     """Runtime over default_cache() with the HIP device detector."""
     return Runtime(default_cache())
+
+
+CODE_OBJECT_DIR = TUNING_FILE.with_suffix(".d")
+
+
+def code_object_cache(cache_dir=CODE_OBJECT_DIR) -> KernelCache:
+    """The persisted cache written by `python -m polykernel_amd.emit` (entries
+    plus their code objects); stale code objects are dropped on load."""
+    cache = KernelCache()
+    cache.load_persisted(cache_dir)
+    cache.invalidate_stale()
+    return cache

@@ -297,3 +297,37 @@ def test_runtime_serves_gemm_and_refuses_mismatch(gpu, oracle):
     with pytest.raises(rt.RuntimeError_) as ei:
         runtime.run("fused_matmul_bias_gelu", M, N, Kd + 64, io)
     assert "no tuned kernel" in ei.value.message
+
+
+# ------------------------------------------------------------------ code objects (emitted, hipModuleLoad)
+
+@pytest.mark.parametrize("op,M,N,Kd,epi", [("matmul_int8_gelu", 16, 28672, 8192, 1),
+                                            ("matmul_int8_residual", 16, 8192, 28672, 2)])
+def test_code_objects_serve_config5_bit_identical(gpu, op, M, N, Kd, epi):
+    """The committed tuned int8 entries, served from the code objects build()
+    emitted (hipModuleLoad + hipModuleLaunchKernel), give the same bits as the
+    linked library kernel at the same configuration."""
+    from polykernel_amd import kernels
+
+    assert rt.CODE_OBJECT_DIR.exists(), "code objects missing: run __graft_entry__.build()"
+    cache = rt.code_object_cache()
+    served = rt.Runtime(cache, code_objects=True)
+    entry = served.resolve(op, M, N, Kd)
+    assert cache.get_binary("gfx950", op, M, N, Kd, "int8") is not None
+    _say(f"code object {op} {entry['best']}")
+    a = synth.normal_bf16((M, Kd), 97)
+    w = synth.normal_bf16((Kd, N), 98, 1.0 / math.sqrt(Kd))
+    wq, s = kernels.quantize_per_channel(to_dev(w))
+    r = synth.normal_bf16((M, N), 99)
+    da, dr = to_dev(a), to_dev(r)
+    out = _empty_bf16((M, N))
+    io = rt.MatmulInt8IO(A=_ptr(da), Wq=_ptr(wq), scale=_ptr(s), C=_ptr(out), residual=_ptr(dr) if epi == 2 else None,
+                         M=M, N=N, K=Kd, workspace=None, workspace_bytes=0, stream=_stream())
+    served.run(op, M, N, Kd, io)
+    got = from_dev(out)
+    direct = from_dev(kernels.matmul_int8_ex(epi, da, wq, s, residual=dr if epi == 2 else None,
+                                             config=entry["best"]))
+    assert np.array_equal(got, direct)
+    # and a second launch (module already loaded) is identical too
+    served.run(op, M, N, Kd, io)
+    assert np.array_equal(from_dev(out), direct)
