@@ -232,6 +232,13 @@ PK_API int pk_gemm_config_ex(int epi, const uint16_t *A, const uint16_t *B, uint
                              const uint16_t *bias, const uint16_t *R, int M, int N, int K,
                              const pk_config *cfg, void *stream);
 
+/* Negative launch probe: launches a trivial kernel with 2048 threads per
+ * workgroup (twice the limit) and stores the hipError_t of the launch and of
+ * the following synchronisation.  PK_OK when the invalid launch was caught
+ * (message in pk_last_error()), PK_ERR_LAUNCH if it was accepted.
+ * Mirrors the `neg` mode of lib/Runtime/hip_run_main.cpp:278-309. */
+PK_API int pk_probe_invalid_launch(int *launch_status, int *sync_status);
+
 /* ---- code-object support ----------------------------------------------------- */
 /* What a host needs to launch the emitted code objects: the device GELU table
  * of the current device (built on first use) and the library-owned

@@ -118,6 +118,7 @@ SIGNATURES = {
     "pk_emit_source": (I, [C.c_char_p]),
     "pk_emit_code_object": (I, [P, C.c_char_p, C.c_char_p, C.c_char_p]),
     "pk_gelu_table": (I, [C.POINTER(P)]),
+    "pk_probe_invalid_launch": (I, [C.POINTER(I), C.POINTER(I)]),
     "pk_library_workspace": (I, [SZ, C.POINTER(P)]),
     "pk_runtime_destroy": (None, [P]),
     "pk_runtime_resolve": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p]),

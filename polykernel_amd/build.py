@@ -79,9 +79,26 @@ def build(verbose: bool = True) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_cli()
     if verbose:
-        print(f"[polykernel_amd] built {LIB} from {len(srcs)} sources", flush=True)
+        print(f"[polykernel_amd] built {LIB} from {len(srcs)} sources, and {CLI}", flush=True)
     return LIB
+
+
+CLI = PKG / "bin" / "pk_hip_run"
+
+
+def build_cli() -> Path:
+    """pk_hip_run: the .npy driver of csrc/cli (links the library and HIP)."""
+    CLI.parent.mkdir(exist_ok=True)
+    tmp = CLI.with_suffix(".tmp")
+    cmd = [CXX, *HOST_FLAGS, str(CSRC / "cli" / "hip_run.cpp"), "-o", str(tmp), str(LIB),
+           "-L", "/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,/opt/rocm/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for pk_hip_run:\n{res.stderr}")
+    os.replace(tmp, CLI)
+    return CLI
 
 
 if __name__ == "__main__":

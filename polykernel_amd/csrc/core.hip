@@ -163,11 +163,39 @@ void parallel_for(int64_t n, F &&f) {
 }
 }  // namespace
 
+// One in-bounds store: the kernel of the invalid-launch probe.
+__global__ void probe_store_kernel(uint16_t *out) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = 0x3F80u;
+}
+
 }  // namespace pk
 
 using namespace pk;
 
 extern "C" {
+
+// Launch probe_store_kernel with 2048 threads per workgroup -- twice the
+// gfx950 limit -- and report what HIP says (lib/Runtime/hip_run_main.cpp:
+// 278-309 of the reference).  The runtime rejects the configuration before
+// dispatch; the kernel itself only ever writes out[0] of an 8-byte buffer.
+int pk_probe_invalid_launch(int *launch_status, int *sync_status) {
+  PK_CHECK_ARG(launch_status && sync_status, "pk_probe_invalid_launch: null argument");
+  uint16_t *d = nullptr;
+  PK_HIP(hipMalloc(&d, 8));
+  probe_store_kernel<<<1, 2048, 0, nullptr>>>(d);
+  const hipError_t le = hipGetLastError();
+  const hipError_t se = hipDeviceSynchronize();
+  (void)hipFree(d);
+  *launch_status = (int)le;
+  *sync_status = (int)se;
+  (void)hipGetLastError();
+  if (le == hipSuccess && se == hipSuccess) {
+    set_error("pk_probe_invalid_launch: a 2048-thread workgroup was accepted");
+    return PK_ERR_LAUNCH;
+  }
+  set_error("invalid launch caught: launch %s, sync %s", hipGetErrorString(le), hipGetErrorString(se));
+  return PK_OK;
+}
 
 const char *pk_version(void) { return "polykernel_amd 0.1.0 gfx950"; }
 
