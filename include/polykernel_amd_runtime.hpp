@@ -216,6 +216,9 @@ class PK_API HipEventTimer {
 struct AutotuneOptions {
   int warmup = 3;
   int iters = 20;
+  // the timed launches of all gated variants are spread over this many
+  // interleaved passes (median over all samples of a variant)
+  int rounds = 5;
   // HBM-bound ops (int8, row-wise, softmax) are timed over rotating copies of
   // their inputs whose total reaches this many bytes (at most 4 copies), so
   // the 256 MiB MALL does not serve them; MFMA-bound ops use one copy.

@@ -61,13 +61,14 @@ def main(argv=None) -> int:
     ap.add_argument("--out", type=Path, help="tuning-cache file to merge the entries into")
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--rounds", type=int, default=5, help="interleaved timing passes over the gated variants")
     ap.add_argument("--max-variants", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
     args = ap.parse_args(argv)
     if args.baseline == bool(args.op):
         ap.error("give either --baseline or --op/--shape")
     jobs = BASELINE if args.baseline else [(args.op, *map(int, args.shape.split(",")))]
-    opts = dict(iters=args.iters, warmup=args.warmup, verbose=args.verbose)
+    opts = dict(iters=args.iters, warmup=args.warmup, rounds=args.rounds, verbose=args.verbose)
     if args.max_variants:
         opts["max_variants"] = args.max_variants
     entries, failed = [], 0

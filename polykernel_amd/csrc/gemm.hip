@@ -522,6 +522,23 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
     }
   };
   __syncthreads();  // every wave is done reading the ring
+  // The epilogue's operands: the bias chunk of a thread's columns is the same
+  // for every row it visits (its column group is tid % 32), so it is loaded
+  // once; the GELU table is copied into ring array Bs2, which the staging
+  // below leaves unused, so each lookup is an LDS read instead of a global
+  // load whose latency every 8-element chunk would wait for.
+  uint16_t *__restrict__ Cp = g.C;
+  const uint16_t *__restrict__ Rp = g.R;
+  const int c_thr = tid & 31;
+  u32x4 bv = {0, 0, 0, 0};
+  if constexpr (EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID)
+    if (g.bias && n0 + 8 * c_thr < g.N) bv = *reinterpret_cast<const u32x4 *>(g.bias + n0 + 8 * c_thr);
+  uint16_t *tab_lds = Bs2;
+  if constexpr (EPI == EPI_BIAS_GELU) {
+    static_assert(GELU_TABLE_SIZE <= B_STAGE, "GELU table fits in one ring array");
+    for (int i = tid; i < (GELU_TABLE_SIZE + 1) / 2; i += G2_THREADS)
+      reinterpret_cast<uint32_t *>(tab_lds)[i] = reinterpret_cast<const uint32_t *>(g.gelu_tab)[i];
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     if (wm == h) {
@@ -545,7 +562,7 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll 4
     for (int j = 0; j < 16; ++j) {
       const int qd = tid + j * G2_THREADS;
-      const int r = qd >> 5, c = qd & 31;
+      const int r = qd >> 5, c = qd & 31;  // c == c_thr
       const int m = m0 + h * 128 + r, n = n0 + 8 * c;
       if (m < g.M && n < g.N) {
         const uint16_t *src = ep_block(r >> 3) + (r & 7) * EP_LD + 8 * c;
@@ -554,11 +571,9 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
         if constexpr (EPI == EPI_NONE) {
           ov = tv;
         } else {
-          u32x4 bv = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
-          if constexpr (EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID)
-            if (g.bias) bv = *reinterpret_cast<const u32x4 *>(g.bias + n);
+          u32x4 rv = {0, 0, 0, 0};
           if constexpr (EPI == EPI_BIAS_RESID || EPI == EPI_RESID)
-            rv = *reinterpret_cast<const u32x4 *>(g.R + (size_t)m * g.N + n);
+            rv = *reinterpret_cast<const u32x4 *>(Rp + (size_t)m * g.N + n);
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             uint32_t o2 = 0;
@@ -567,7 +582,7 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
               const float t = hh ? hi_bf(tv[w]) : lo_bf(tv[w]);
               uint32_t o;
               if constexpr (EPI == EPI_BIAS_GELU) {
-                o = gelu_bits(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))), g.gelu_tab);
+                o = gelu_bits(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))), tab_lds);
               } else if constexpr (EPI == EPI_BIAS_RESID) {
                 const float u = bf2f(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))));
                 o = f2bf(u + (hh ? hi_bf(rv[w]) : lo_bf(rv[w])));
@@ -579,7 +594,7 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
             ov[w] = o2;
           }
         }
-        *reinterpret_cast<u32x4 *>(g.C + (size_t)m * g.N + n) = ov;
+        *reinterpret_cast<u32x4 *>(Cp + (size_t)m * g.N + n) = ov;
       }
     }
     if (h == 0) __syncthreads();  // the half is consumed before the next overwrites it

@@ -14,8 +14,9 @@
 //   3. every candidate of ConfigSpace::Candidates -- the library's default
 //      first -- runs once into an output poisoned with NaN, is compared with
 //      the golden (pk_compare_bf16: cosine, max_rel_err, pcc) and gated;
-//   4. a variant that passes is timed with HIP events, `warmup` launches
-//      then the median of `iters`.  HBM-bound ops (int8 weight streaming,
+//   4. the variants that passed are timed with HIP events: `warmup` launches
+//      each, then `iters` launches each spread over `rounds` interleaved
+//      passes, the median per variant.  HBM-bound ops (int8 weight streaming,
 //      row-wise norms, softmax) rotate over copies of their inputs large
 //      enough that the 256 MiB MALL cannot hold them -- otherwise they would
 //      be timed from cache; MFMA-bound ops (GEMMs, attention, RMSNorm->MatMul)
@@ -404,31 +405,52 @@ bool Autotune(std::string_view op, const Shape &shape, const AutotuneOptions &o,
     }
     v.correctness = Correctness{m[0], m[1], m[2]};
     v.validated = PassesCorrectnessGate(v.correctness, ceiling);
-    if (v.validated) {
-      for (int i = 0; i < o.warmup; ++i) (void)w.run(&pc, i % w.copies, st);
-      std::vector<float> times;
-      for (int i = 0; i < std::max(1, o.iters); ++i) {
+    if (o.verbose)
+      std::fprintf(stderr, "[autotune] %s %s cosine=%.6f max_rel=%.3e pcc=%.6f %s\n", std::string(op).c_str(),
+                   v.name.c_str(), m[0], m[1], m[2], v.validated ? "PASS" : "REJECTED");
+    results.push_back(v);
+  }
+
+  // Timing, only of the variants that passed: `rounds` interleaved passes over
+  // all of them (each pass: one warm-up launch, then its share of `iters`), so
+  // that clock and thermal drift during the sweep reaches every variant alike
+  // instead of favouring the ones measured first.
+  std::vector<size_t> timed;
+  for (size_t i = 0; i < results.size(); ++i)
+    if (results[i].validated) timed.push_back(i);
+  const int rounds = std::max(1, std::min(o.rounds, std::max(1, o.iters)));
+  const int per_round = std::max(1, (std::max(1, o.iters) + rounds - 1) / rounds);
+  std::vector<std::vector<float>> samples(results.size());
+  for (size_t i : timed) {  // initial warm-up of every variant
+    const pk_config pc = ToPk(cands[i]);
+    for (int k = 0; k < o.warmup; ++k) (void)w.run(&pc, k % w.copies, st);
+  }
+  for (int r = 0; r < rounds; ++r) {
+    for (size_t i : timed) {
+      if (!results[i].validated) continue;
+      const pk_config pc = ToPk(cands[i]);
+      (void)w.run(&pc, 0, st);
+      for (int k = 0; k < per_round; ++k) {
         HipEventTimer t;
         t.Start(st);
-        rc = w.run(&pc, i % w.copies, st);
+        const int rc = w.run(&pc, (r * per_round + k) % w.copies, st);
         t.Stop(st);
         const float ms = t.ElapsedMs();
         if (rc != PK_OK || ms < 0) {
-          v.validated = false;
+          results[i].validated = false;
           break;
         }
-        times.push_back(ms);
-      }
-      if (v.validated) {
-        std::sort(times.begin(), times.end());
-        v.time_ms = times[times.size() / 2];
+        samples[i].push_back(ms);
       }
     }
+  }
+  for (size_t i : timed) {
+    if (!results[i].validated || samples[i].empty()) continue;
+    std::sort(samples[i].begin(), samples[i].end());
+    results[i].time_ms = samples[i][samples[i].size() / 2];
     if (o.verbose)
-      std::fprintf(stderr, "[autotune] %s %s cosine=%.6f max_rel=%.3e pcc=%.6f %s%s\n", std::string(op).c_str(),
-                   v.name.c_str(), m[0], m[1], m[2], v.validated ? "PASS" : "REJECTED",
-                   v.time_ms ? (" " + std::to_string(*v.time_ms) + " ms").c_str() : "");
-    results.push_back(v);
+      std::fprintf(stderr, "[autotune] %s %s %.6f ms (median of %zu)\n", std::string(op).c_str(),
+                   results[i].name.c_str(), *results[i].time_ms, samples[i].size());
   }
   if (!HipOk(hipStreamSynchronize(st), "sweep", error)) return false;
 

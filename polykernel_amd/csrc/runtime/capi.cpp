@@ -239,6 +239,7 @@ PK_API int pk_autotune(const char *op, long long M, long long N, long long K, co
       const auto d = v.as_number();
       if (k == "warmup" && i) o.warmup = (int)*i;
       else if (k == "iters" && i) o.iters = (int)*i;
+      else if (k == "rounds" && i && *i > 0) o.rounds = (int)*i;
       else if (k == "rotate_bytes" && i && *i >= 0) o.rotate_bytes = (size_t)*i;
       else if (k == "rel_ceiling" && d) o.rel_ceiling = *d;
       else if (k == "max_variants" && i && *i > 0) o.max_variants = (size_t)*i;
