@@ -60,6 +60,10 @@ PK_API int pk_parse_gcn_arch_name(const char *gcn_arch_name, char *buf, int buf_
  * fp32 -> bf16 conversion differs from the reference RNE formula
  * (kernels/cpu/cpu_reference.h:52-61).  Synchronous; allocates 8 bytes. */
 PK_API int pk_check_bf16_conversion(unsigned long long *mismatches);
+/* Device self-check of the two-codes-per-register GELU the GEMM epilogue
+ * uses: counts the pairs (every low code x four high-code patterns) where it
+ * differs from the per-element exact GELU.  Synchronous; allocates 8 bytes. */
+PK_API int pk_check_gelu_pairs(unsigned long long *mismatches);
 
 /* ---- reference entry points (same names and argument order) ------------ */
 

@@ -65,6 +65,25 @@ __global__ void bf16_selfcheck_kernel(unsigned long long *bad) {
   if (n) atomicAdd(bad, n);
 }
 
+// Self-check of the paired GELU: for every low code (all 65536) and four
+// high-code patterns, gelu_pair_common (where neither code is a NaN or an
+// infinity) and the dispatch the GEMM epilogue uses must equal gelu_bits of
+// each code.
+__global__ void gelu_pair_selfcheck_kernel(const uint16_t *tab, unsigned long long *bad) {
+  const uint32_t lo = blockIdx.x * blockDim.x + threadIdx.x;
+  if (lo >= 65536u) return;
+  unsigned long long n = 0;
+  const uint32_t his[4] = {lo, lo ^ 0x8000u, (lo * 40503u + 7u) & 0xFFFFu, 0xFFFFu - lo};
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t w = lo | (his[k] << 16);
+    const uint32_t want = gelu_pair_exact(w, tab);
+    if (!gelu_pair_special(w)) n += gelu_pair_common(w, tab) != want;
+    const uint32_t got = gelu_pair_special(w) ? gelu_pair_exact(w, tab) : gelu_pair_common(w, tab);
+    n += got != want;
+  }
+  if (n) atomicAdd(bad, n);
+}
+
 int gelu_table(const uint16_t **table) {
   int dev = 0;
   PK_HIP(hipGetDevice(&dev));
@@ -244,6 +263,24 @@ int pk_check_bf16_conversion(unsigned long long *mismatches) {
 // through the run of lower-case letters and digits after it
 // ("gfx950:sramecc+:xnack-" -> "gfx950"); "" when there is none
 // (lib/Runtime/DeviceDetect.cpp:28-50 of the reference).
+int pk_check_gelu_pairs(unsigned long long *mismatches) {
+  PK_CHECK_ARG(mismatches, "pk_check_gelu_pairs: null argument");
+  const uint16_t *tab = nullptr;
+  int rc = gelu_table(&tab);
+  if (rc) return rc;
+  unsigned long long *d = nullptr;
+  PK_HIP(hipMalloc(&d, sizeof(unsigned long long)));
+  hipError_t e = hipMemset(d, 0, sizeof(unsigned long long));
+  if (e == hipSuccess) {
+    gelu_pair_selfcheck_kernel<<<65536 / 256, 256>>>(tab, d);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(mismatches, d, sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "pk_check_gelu_pairs");
+  return PK_OK;
+}
+
 int pk_parse_gcn_arch_name(const char *name, char *buf, int buf_len) {
   if (!name || !buf || buf_len <= 0) {
     set_error("pk_parse_gcn_arch_name: null argument");

@@ -533,6 +533,12 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   u32x4 bv = {0, 0, 0, 0};
   if constexpr (EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID)
     if (g.bias && n0 + 8 * c_thr < g.N) bv = *reinterpret_cast<const u32x4 *>(g.bias + n0 + 8 * c_thr);
+  float bias_f[8];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    bias_f[2 * w] = lo_bf(bv[w]);
+    bias_f[2 * w + 1] = hi_bf(bv[w]);
+  }
   uint16_t *tab_lds = Bs2;
   if constexpr (EPI == EPI_BIAS_GELU) {
     static_assert(GELU_TABLE_SIZE <= B_STAGE, "GELU table fits in one ring array");
@@ -559,6 +565,44 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
         }
     }
     __syncthreads();
+    if constexpr (EPI == EPI_BIAS_GELU) {
+      // The whole half at once: all 16 chunks of a thread are read and biased
+      // first, one wave vote picks the paired GELU (no NaN or infinity in the
+      // wave's half) or the exact per-element one for all of them, then every
+      // table lookup is issued before any result is stored.
+      uint32_t u[16][4];
+      uint32_t special = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = (tid + j * G2_THREADS) >> 5;
+        const u32x4 tv = *reinterpret_cast<const u32x4 *>(ep_block(r >> 3) + (r & 7) * EP_LD + 8 * c_thr);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          u[j][w] = pack_bf(lo_bf(tv[w]) + bias_f[2 * w], hi_bf(tv[w]) + bias_f[2 * w + 1]);
+          special |= gelu_pair_special(u[j][w]);
+        }
+      }
+      if (__builtin_amdgcn_ballot_w64(special != 0) == 0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) u[j][w] = gelu_pair_common(u[j][w], tab_lds);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) u[j][w] = gelu_pair_exact(u[j][w], tab_lds);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = (tid + j * G2_THREADS) >> 5;
+        const int m = m0 + h * 128 + r, n = n0 + 8 * c_thr;
+        if (m < g.M && n < g.N)
+          *reinterpret_cast<u32x4 *>(Cp + (size_t)m * g.N + n) = u32x4{u[j][0], u[j][1], u[j][2], u[j][3]};
+      }
+      if (h == 0) __syncthreads();  // the half is consumed before the next overwrites it
+      continue;
+    }
 #pragma unroll 4
     for (int j = 0; j < 16; ++j) {
       const int qd = tid + j * G2_THREADS;
@@ -574,24 +618,24 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
           u32x4 rv = {0, 0, 0, 0};
           if constexpr (EPI == EPI_BIAS_RESID || EPI == EPI_RESID)
             rv = *reinterpret_cast<const u32x4 *>(Rp + (size_t)m * g.N + n);
+          {
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            uint32_t o2 = 0;
+            for (int w = 0; w < 4; ++w) {
+              uint32_t o2 = 0;
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-              const float t = hh ? hi_bf(tv[w]) : lo_bf(tv[w]);
-              uint32_t o;
-              if constexpr (EPI == EPI_BIAS_GELU) {
-                o = gelu_bits(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))), tab_lds);
-              } else if constexpr (EPI == EPI_BIAS_RESID) {
-                const float u = bf2f(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))));
-                o = f2bf(u + (hh ? hi_bf(rv[w]) : lo_bf(rv[w])));
-              } else {
-                o = f2bf(t + (hh ? hi_bf(rv[w]) : lo_bf(rv[w])));
+              for (int hh = 0; hh < 2; ++hh) {
+                const float t = hh ? hi_bf(tv[w]) : lo_bf(tv[w]);
+                uint32_t o;
+                if constexpr (EPI == EPI_BIAS_RESID) {
+                  const float u = bf2f(f2bf(t + (hh ? hi_bf(bv[w]) : lo_bf(bv[w]))));
+                  o = f2bf(u + (hh ? hi_bf(rv[w]) : lo_bf(rv[w])));
+                } else {
+                  o = f2bf(t + (hh ? hi_bf(rv[w]) : lo_bf(rv[w])));
+                }
+                o2 |= o << (16 * hh);
               }
-              o2 |= o << (16 * hh);
+              ov[w] = o2;
             }
-            ov[w] = o2;
           }
         }
         *reinterpret_cast<u32x4 *>(Cp + (size_t)m * g.N + n) = ov;

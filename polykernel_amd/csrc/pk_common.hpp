@@ -132,6 +132,51 @@ __device__ __forceinline__ uint32_t gelu_bits(uint32_t u, const uint16_t *__rest
   return in_tab ? tv : r;
 }
 
+// Two GELU codes per register (low half = element 0), with 16-bit packed
+// integer ops, for the common case: neither code is a NaN or an infinity.
+// Same results as gelu_bits there:
+//   mag < TLO           -> bf16(0.5 x), the float formula of gelu_bits
+//   table range         -> tab[(neg ? NPOS : 0) + mag - TLO]
+//   above it            -> x (positive) or -0 (negative)
+// 15-bit magnitudes make "a < b" the sign bit of the packed difference; the
+// table index is clamped into range with a packed min, so every lookup is in
+// bounds, and the selects are bit-field inserts of both halves at once.
+typedef unsigned short pk_u16x2 __attribute__((ext_vector_type(2)));
+typedef short pk_i16x2 __attribute__((ext_vector_type(2)));
+
+// Nonzero when either code of the pair is a NaN or an infinity (magnitude
+// >= 0x7F80): mag + 0x80 reaches bit 15 of its half exactly then, and no
+// carry crosses from the low half into the high one.
+__device__ __forceinline__ uint32_t gelu_pair_special(uint32_t w) {
+  return ((w & 0x7FFF7FFFu) + 0x00800080u) & 0x80008000u;
+}
+
+__device__ __forceinline__ uint32_t gelu_pair_common(uint32_t w, const uint16_t *__restrict__ tab) {
+  typedef pk_u16x2 u2;
+  const u2 mag = __builtin_bit_cast(u2, w & 0x7FFF7FFFu);
+  const uint32_t sgn = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_i16x2, w) >> (pk_i16x2){15, 15});
+  const u2 sg = __builtin_bit_cast(u2, sgn);
+  const u2 off = mag - (u2){(unsigned short)GELU_TLO, (unsigned short)GELU_TLO};
+  const u2 lim = (u2){(unsigned short)(GELU_PHI - GELU_TLO), (unsigned short)(GELU_PHI - GELU_TLO)} +
+                 (sg & (u2){(unsigned short)(GELU_NHI - GELU_PHI), (unsigned short)(GELU_NHI - GELU_PHI)});
+  const u2 idx0 = __builtin_elementwise_min(off, lim);
+  // 0xFFFF where off <= lim (the code is in the table), 0 elsewhere
+  const u2 m_tab = __builtin_elementwise_min(off ^ idx0, (u2){1, 1}) - (u2){1, 1};
+  const u2 idx = idx0 + (sg & (u2){(unsigned short)GELU_NPOS, (unsigned short)GELU_NPOS});
+  const uint32_t tv = (uint32_t)tab[idx.x] | ((uint32_t)tab[idx.y] << 16);
+  const uint32_t half = pack_bf(0.5f * lo_bf(w), 0.5f * hi_bf(w));
+  const uint32_t m_small = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_i16x2, off) >> (pk_i16x2){15, 15});
+  const uint32_t big = (sgn & 0x80008000u) | (~sgn & w);
+  const uint32_t r = (m_small & half) | (~m_small & big);
+  const uint32_t mt = __builtin_bit_cast(uint32_t, m_tab);
+  return (mt & tv) | (~mt & r);
+}
+
+// Both codes of a pair through the exact per-element rules.
+__device__ __forceinline__ uint32_t gelu_pair_exact(uint32_t w, const uint16_t *__restrict__ tab) {
+  return gelu_bits(w & 0xFFFFu, tab) | (gelu_bits(w >> 16, tab) << 16);
+}
+
 // ---- direct-to-LDS loads ----------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
