@@ -68,6 +68,18 @@ def test_device_bf16_conversion_exhaustive(gpu):
     assert bad.value == 0
 
 
+def test_paired_gelu_equals_exact_gelu(gpu):
+    """The GEMM epilogue's two-codes-per-register GELU equals the per-element
+    exact GELU for every code in the low half (x four high-half patterns), on
+    its common path and through its NaN/infinity fallback."""
+    import ctypes
+    from polykernel_amd import _lib
+
+    bad = ctypes.c_ulonglong(123)
+    _lib.check(_lib.load().pk_check_gelu_pairs(ctypes.byref(bad)), "pk_check_gelu_pairs")
+    assert bad.value == 0
+
+
 def test_gelu_all_bf16_codes_bit_exact(gpu, oracle):
     x = np.arange(1 << 16, dtype=np.uint16)
     got = from_dev(K().gelu(to_dev(x)))
