@@ -503,9 +503,7 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
   // S^T block = K Q^T (raw scores, unscaled)
   auto qk = [&](int stage) __attribute__((always_inline)) -> f32x16 {
     const uint8_t *ks = ring + stage * 2 * TB;
-    f32x16 sc;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = 0.f;
+    f32x16 sc{};
     const int row = 32 * kh + (lane & 31);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
@@ -582,25 +580,57 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     }
   };
 
-  // ---- pipeline: step s waits for its own loads, one barrier, then the
-  // stage of step s-1 (free: every wave is past it) is refilled with step
-  // s+STAGES-1 and step s is computed.
+  // ---- pipeline, scores one step ahead.  Iteration s waits for step s+1's
+  // loads, passes one barrier, refills the stage of step s-1 (every wave is
+  // past it) with step s+STAGES-1, issues the K Q^T MFMAs of step s+1 and
+  // then runs the softmax and P V of step s, whose VALU work the matrix
+  // core overlaps with those MFMAs.  Steps [0, n_full) are visible and
+  // unmasked for every wave of the workgroup and take a body with no
+  // per-wave branch (the accumulator then stays in place); the remaining
+  // steps (causal diagonal, ragged end) test each wave's block.
   using MaskT = std::integral_constant<bool, true>;
   using NoMaskT = std::integral_constant<bool, false>;
-#pragma unroll
-  for (int p = 0; p < STAGES - 1; ++p)
-    if (p < nsteps) issue(p, p);
-  for (int s = 0; s < nsteps; ++s) {
-    if (s + STAGES - 2 < nsteps) vm_wait<(STAGES - 2) * NPW>();
+  static_assert(STAGES >= 3, "one step in flight beyond the next");
+  const int lim = causal ? min(kv_end, off + q0 + 1) : kv_end;  // keys every query of the group sees
+  const int n_full = max(0, min(nsteps, lim / BKV - t_begin));
+  auto sync_next = [&](int s) __attribute__((always_inline)) {
+    if (s + STAGES - 2 < nsteps) vm_wait<(STAGES - 3) * NPW>();
     else vm_wait<0>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS access moves above the barrier
     if (s + STAGES - 1 < nsteps) issue(s + STAGES - 1, (s + STAGES - 1) % STAGES);
+  };
+  f32x16 sc{};
+  if (nsteps > 0) {
+#pragma unroll
+    for (int p = 0; p < STAGES - 1; ++p)
+      if (p < nsteps) issue(p, p);
+    if (STAGES - 2 < nsteps) vm_wait<(STAGES - 2) * NPW>();
+    else vm_wait<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    sc = qk(0);
+  }
+  const int n_hot = min(n_full, nsteps - 1);
+  int s = 0;
+  for (; s < n_hot; ++s) {
+    sync_next(s);
+    const f32x16 nxt = qk((s + 1) % STAGES);
+    softmax_pv(NoMaskT{}, s, s % STAGES, sc);
+    sc = nxt;
+  }
+  for (; s < nsteps; ++s) {
+    const bool more = s + 1 < nsteps;  // uniform: every wave passes the same barriers
+    f32x16 nxt = sc;
+    if (more) {
+      sync_next(s);
+      nxt = qk((s + 1) % STAGES);
+    }
     if (visible(s)) {
-      const f32x16 sc = qk(s % STAGES);
       if (masked(s)) softmax_pv(MaskT{}, s, s % STAGES, sc);
       else softmax_pv(NoMaskT{}, s, s % STAGES, sc);
     }
+    sc = nxt;
   }
   vm_wait<0>();
   __syncthreads();  // every wave is done with the ring
