@@ -60,8 +60,11 @@ struct AttArgs {
 template <int DP>
 __device__ __forceinline__ int swz_v(int k) {
   if constexpr (DP >= 128) {
-    constexpr int t[4] = {0, 4, 10, 14};
-    return t[k & 3];
+    // 0, 4, 10, 14 for k & 3 = 0..3, as arithmetic: a table would live in
+    // memory and be re-read (with a wait on every load in flight) after
+    // each barrier of the pipelined loops
+    const int j = k & 3;
+    return (j << 2) | ((j >> 1) << 1);
   } else if constexpr (DP == 64) {
     return (k & 3) * 2;
   } else {
