@@ -198,9 +198,14 @@ PK_API int pk_gemm_set_ring_depth(int depth);
  *     second kernel); shared_memory_stages = per-wave ring depth in 64-row
  *     steps; block_m = rows of A per workgroup (16, 32 or 64); vector_width
  *     = 16 (int8 per DMA lane); unroll = 2 (16x16x32 MFMA k-steps per step).
- *   fused_rmsnorm_matmul, fused_residual_rmsnorm, fused_softmax_mask,
- *     fused_kv_append_attention: one fixed configuration per shape that
- *     describes the kernel the entry point runs (see pk_op_configs). */
+ *   fused_kv_append_attention (D 64 or 128): the flash kernel's two tile
+ *     shapes -- block_m queries x block_n keys per step, 128 x 64 or 64 x 128
+ *     (block_k = D, num_warps = 8 waves, vector_width = 8, unroll = D / 16
+ *     MFMA k-steps per product, shared_memory_stages = slots of the K ring
+ *     and of the V ring); other D: the generic kernel's one configuration.
+ *   fused_rmsnorm_matmul, fused_residual_rmsnorm, fused_softmax_mask: one
+ *     fixed configuration per shape that describes the kernel the entry
+ *     point runs (see pk_op_configs). */
 typedef struct pk_config {
   int block_m, block_n, block_k, num_warps, vector_width, unroll, shared_memory_stages;
 } pk_config;
@@ -235,6 +240,16 @@ PK_API int pk_matmul_int8_ex(int epi, const uint16_t *A, const int8_t *Wq, const
 PK_API int pk_gemm_config_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C,
                              const uint16_t *bias, const uint16_t *R, int M, int N, int K,
                              const pk_config *cfg, void *stream);
+
+/* launch_fused_kv_append_attention with an explicit configuration (one of
+ * pk_op_configs("fused_kv_append_attention", S_q, S_cache + S_q, D); NULL =
+ * built-in choice).  A flash configuration the operands do not allow
+ * (alignment, scale <= 0, S_cache not a multiple of block_n) returns
+ * PK_ERR_UNSUPPORTED; anything else not in the list PK_ERR_INVALID_ARG. */
+PK_API int pk_fused_kv_append_attention_config(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc, const uint16_t *Kn,
+                                               const uint16_t *Vn, uint16_t *O, int B, int H, int S_q,
+                                               int S_cache, int D, int cache_capacity, float scale, int causal,
+                                               const pk_config *cfg, void *stream);
 
 /* Negative launch probe: launches a trivial kernel with 2048 threads per
  * workgroup (twice the limit) and stores the hipError_t of the launch and of

@@ -24,6 +24,8 @@
 // alone do not fill the chip the key range is split (flash-decoding style)
 // and att_combine_kernel merges the fp32 partials in split order.  Head dims
 // 64 and 128 with enough query tiles take attention_fa_kernel (below).
+#include <cstring>
+
 #include "pk_common.hpp"
 
 namespace pk {
@@ -35,6 +37,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int AT_WAVES = 4;
@@ -341,11 +344,12 @@ __global__ __launch_bounds__(256) void att_combine_kernel(AttArgs g) {
 // range in steps of 32*KH keys (QG * KH = 8): wave (qg, kh) handles query
 // group qg (32 queries, the S^T layout above) against keys
 // [step*32*KH + 32*kh, +32) with its own running max / sum / accumulator.
-// Two waves share each SIMD, so one can run the softmax while the other
-// issues MFMAs.  K and V tiles arrive in a ring of LDS stages by
-// buffer_load ... lds (waves 0-3 load K, 4-7 V), one barrier per step; the
-// ring holds 128 KiB, i.e. STAGES-1 steps of prefetch.  Diagonal blocks are
-// masked, blocks above the diagonal skipped.  At the end the KH partial
+// Tile shapes: QG 4 (128 queries x 64 keys per step) or QG 2 (64 x 128).
+// Two waves share each SIMD.  K and V tiles arrive by buffer_load ... lds
+// (waves 0-3 load K, 4-7 V) into two rings of 64 KiB, one barrier per step;
+// within a wave the score MFMAs of the next step and the P V MFMAs of the
+// previous one overlap the softmax of the current step.  Diagonal blocks
+// are masked, blocks above the diagonal skipped.  At the end the KH partial
 // states of each query are merged in LDS in kh order.  When the grid would
 // not fill the chip, the key range is also split over `splits` workgroups
 // whose fp32 partials fa_combine_kernel merges in split order.
@@ -377,12 +381,12 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
   constexpr int BKV = 32 * KH;               // keys per step
   constexpr int CH = DP / 8;                 // 16-byte chunks per row
   constexpr int TB = BKV * DP * 2;           // bytes of one K (or V) tile
-  constexpr int STAGES = FA_RING / (2 * TB);
+  constexpr int SL = FA_RING / (2 * TB);     // slots of the K ring and of the V ring
   constexpr int NK = TB / 1024;              // DMA instructions per tile
   constexpr int NPW = NK / (FA_WAVES / 2);   // per wave per step
   constexpr int RPI = 1024 / (2 * DP);       // rows per DMA instruction
   constexpr int DS = DP / 16, DB = DP / 32;
-  static_assert(STAGES >= 2 && NPW >= 1 && NK % (FA_WAVES / 2) == 0, "ring shape");
+  static_assert(SL >= 2 && NPW >= 1 && NK % (FA_WAVES / 2) == 0, "ring shape");
   constexpr int PS = DP + 4;                 // merge-buffer row stride (floats), 16 B padding
   constexpr int MERGE = FA_WAVES * 32 * PS * 4;
   // the ring, reused as the merge buffer after the last step
@@ -462,12 +466,12 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     lrow[j] = row;
     voff0[j] = (uint32_t)(row * DP * 2 + 16 * lc);
   }
-  auto issue = [&](int step, int stage) __attribute__((always_inline)) {
+  auto issue = [&](int step, int slot) __attribute__((always_inline)) {
     const int k0 = (t_begin + step) * BKV;
     const bool nw = FUSED && k0 >= S_cache;
     const pk_u32x4 rs = nw ? rs_n : rs_c;
     const int r0 = nw ? k0 - S_cache : k0;  // first row of the step in its source
-    uint8_t *tile = ring + stage * 2 * TB + (isk ? 0 : TB);
+    uint8_t *tile = ring + (isk ? slot : SL + slot) * TB;
     if (k0 + BKV <= kv_end) {
 #pragma unroll
       for (int j = 0; j < NPW; ++j)
@@ -480,6 +484,16 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
                   (uint32_t)(r0 * DP * 2));
       }
     }
+  };
+  // instructions [j0, j1) of the DMA of a step that lies wholly below kv_end
+  auto issue_rows = [&](int step, int slot, int j0, int j1) __attribute__((always_inline)) {
+    const int k0 = (t_begin + step) * BKV;
+    const bool nw = FUSED && k0 >= S_cache;
+    const pk_u32x4 rs = nw ? rs_n : rs_c;
+    const int r0 = nw ? k0 - S_cache : k0;
+    uint8_t *tile = ring + (isk ? slot : SL + slot) * TB;
+#pragma unroll
+    for (int j = j0; j < j1; ++j) dma_lds16(rs, tile + (wq * NPW + j) * 1024, voff0[j], (uint32_t)(r0 * DP * 2));
   };
 
   f32x16 acc_o[DB];
@@ -504,8 +518,8 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     return kb0 + 31 >= kv_end || (causal && kb0 + 31 > off + qw);
   };
   // S^T block = K Q^T (raw scores, unscaled)
-  auto qk = [&](int stage) __attribute__((always_inline)) -> f32x16 {
-    const uint8_t *ks = ring + stage * 2 * TB;
+  auto qk = [&](int slot) __attribute__((always_inline)) -> f32x16 {
+    const uint8_t *ks = ring + slot * TB;
     f32x16 sc{};
     const int row = 32 * kh + (lane & 31);
 #pragma unroll
@@ -520,11 +534,16 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
   // used in the exponent is raised only when a new score exceeds it by more
   // than 8 / c (p may reach 2^8 meanwhile); o = sum p v / sum p does not
   // depend on it, and skipping most rescales saves the multiply of the whole
-  // accumulator.  Then O^T += V^T (P_hi + P_lo)^T.  MASKED is a compile-time
-  // flag so blocks off the diagonal carry no mask arithmetic.
-  auto softmax_pv = [&](auto mask_c, int step, int stage, f32x16 sc) __attribute__((always_inline)) {
+  // accumulator.  Each weight is split into bf16 halves p = p_hi + p_lo for
+  // the P V product.  MASKED is a compile-time flag so blocks off the
+  // diagonal carry no mask arithmetic.  Returns the factor the accumulator
+  // must be multiplied by (after the products of earlier steps are in it),
+  // 1 when the max did not move.
+  struct Pw {
+    bf16x8 hi[2], lo[2];
+  };
+  auto softmax = [&](auto mask_c, int step, f32x16 sc, Pw &pw, bool &resc) __attribute__((always_inline)) -> float {
     constexpr bool MASKED = decltype(mask_c)::value;
-    const uint8_t *vs = ring + stage * 2 * TB + TB;
     float tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -535,14 +554,11 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
       tmax = fmaxf(tmax, sc[i]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    if (__any((tmax - m_run) * c2 > 8.0f)) {  // also true for the first block (m_run = -inf)
+    float alpha = 1.f;
+    resc = __any((tmax - m_run) * c2 > 8.0f);  // also true for the first block (m_run = -inf)
+    if (resc) {
       const float m_new = fmaxf(m_run, tmax);
-      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run - m_new) * c2);
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc_o[db][e] *= alpha;
+      alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run - m_new) * c2);
       m_run = m_new;
     }
     const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
@@ -558,13 +574,19 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
       plo[i >> 1] = pack_bf(p0 - lo_bf(hh), p1 - hi_bf(hh));
     }
     psum += __shfl_xor(psum, 32, 64);
-    l_run += psum;
+    l_run = l_run * alpha + psum;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      const u32x4 hv4 = {phi[4 * st + 0], phi[4 * st + 1], phi[4 * st + 2], phi[4 * st + 3]};
-      const u32x4 lv4 = {plo[4 * st + 0], plo[4 * st + 1], plo[4 * st + 2], plo[4 * st + 3]};
-      const bf16x8 pb_hi = __builtin_bit_cast(bf16x8, hv4);
-      const bf16x8 pb_lo = __builtin_bit_cast(bf16x8, lv4);
+      pw.hi[st] = __builtin_bit_cast(bf16x8, (u32x4{phi[4 * st], phi[4 * st + 1], phi[4 * st + 2], phi[4 * st + 3]}));
+      pw.lo[st] = __builtin_bit_cast(bf16x8, (u32x4{plo[4 * st], plo[4 * st + 1], plo[4 * st + 2], plo[4 * st + 3]}));
+    }
+    return alpha;
+  };
+  // O^T += V^T (P_hi + P_lo)^T for one step's V tile
+  auto pv = [&](const Pw &pw, int slot) __attribute__((always_inline)) {
+    const uint8_t *vs = ring + (SL + slot) * TB;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         i16x4 hv[2];
@@ -577,133 +599,171 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
               (lds_i16x4 *)(vs + key * DP * 2 + 16 * (c ^ swz_v<DP>(key)) + 2 * (d & 7)));
         }
         const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(hv[0], hv[1], 0, 1, 2, 3, 4, 5, 6, 7));
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb_hi, acc_o[db], 0, 0, 0);
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb_lo, acc_o[db], 0, 0, 0);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pw.hi[st], acc_o[db], 0, 0, 0);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pw.lo[st], acc_o[db], 0, 0, 0);
       }
     }
   };
+  auto rescale = [&](float alpha) __attribute__((always_inline)) {
+    // alpha is 1 on the path that skips the rescale; an opaque copy keeps
+    // the compiler from turning the rare branch into a multiply of the whole
+    // accumulator on every step
+    asm volatile("" : "+v"(alpha));
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_o[db][e] *= alpha;
+  };
 
-  // ---- pipeline, scores one step ahead.  Iteration s waits for step s+1's
-  // loads, passes one barrier, refills the stage of step s-1 (every wave is
-  // past it) with step s+STAGES-1, issues the K Q^T MFMAs of step s+1 and
-  // then runs the softmax and P V of step s, whose VALU work the matrix
-  // core overlaps with those MFMAs.  Steps [0, n_full) are visible and
-  // unmasked for every wave of the workgroup and take a body with no
-  // per-wave branch (the accumulator then stays in place); the remaining
-  // steps (causal diagonal, ragged end) test each wave's block.
+  // ---- pipeline.  K tiles and V tiles live in separate rings of SL slots
+  // (step t in slot t % SL of each).  Iteration s (0 <= s <= nsteps) waits
+  // for K(s+1) and V(s-1), passes one barrier, refills the K slot of step s
+  // (its scores were computed in iteration s-1) with K(s+SL) and the V slot
+  // of step s-2 (its P V ran in iteration s-1) with V(s+SL-2), then issues
+  // the K Q^T MFMAs of step s+1 and the P V MFMAs of step s-1 -- 24 MFMAs
+  // that depend on nothing the softmax of step s computes -- and runs that
+  // softmax on the scores of the previous iteration, so the matrix core
+  // works while the VALU does.  A rescale of the accumulator waits for
+  // P V(s-1), at the end of the iteration.  Steps [0, n_full) are visible
+  // and unmasked for every wave of the workgroup and iterations over them
+  // take a body with no per-wave branch; the others test each wave's blocks.
   using MaskT = std::integral_constant<bool, true>;
   using NoMaskT = std::integral_constant<bool, false>;
-  static_assert(STAGES >= 3, "one step in flight beyond the next");
   const int lim = causal ? min(kv_end, off + q0 + 1) : kv_end;  // keys every query of the group sees
   const int n_full = max(0, min(nsteps, lim / BKV - t_begin));
-  auto sync_next = [&](int s) __attribute__((always_inline)) {
-    if (s + STAGES - 2 < nsteps) vm_wait<(STAGES - 3) * NPW>();
+  // this wave's loads: K(t) for waves 0-3 (issued SL steps ahead), V(t)
+  // for waves 4-7 (SL-2 ahead); the step iteration s needs from them
+  const int lead = isk ? SL : SL - 2;
+  auto wait_barrier = [&](int s) __attribute__((always_inline)) {
+    const int need = isk ? s + 1 : s - 1;
+    const int last = min(nsteps - 1, s + lead - 1);  // newest step issued so far
+    if (last - need >= SL - 2) vm_wait<(SL - 2) * NPW>();
     else vm_wait<0>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS access moves above the barrier
-    if (s + STAGES - 1 < nsteps) issue(s + STAGES - 1, (s + STAGES - 1) % STAGES);
+  };
+  // islot: the slot of step s + lead, (s + lead) % SL
+  auto sync = [&](int s, int islot) __attribute__((always_inline)) {
+    wait_barrier(s);
+    if (s + lead < nsteps) issue(s + lead, islot);
   };
   f32x16 sc{};
+  Pw pw_prev;
   if (nsteps > 0) {
 #pragma unroll
-    for (int p = 0; p < STAGES - 1; ++p)
-      if (p < nsteps) issue(p, p);
-    if (STAGES - 2 < nsteps) vm_wait<(STAGES - 2) * NPW>();
-    else vm_wait<0>();
+    for (int t = 0; t < SL; ++t)
+      if (t < lead && t < nsteps) issue(t, t);
+    if (isk) {
+      if (nsteps - 1 >= SL - 1) vm_wait<(SL - 1) * NPW>();
+      else vm_wait<0>();
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     sc = qk(0);
   }
-  const int n_hot = min(n_full, nsteps - 1);
-  int s = 0;
-  for (; s < n_hot; ++s) {
-    sync_next(s);
-    const f32x16 nxt = qk((s + 1) % STAGES);
-    softmax_pv(NoMaskT{}, s, s % STAGES, sc);
-    sc = nxt;
-  }
-  for (; s < nsteps; ++s) {
-    const bool more = s + 1 < nsteps;  // uniform: every wave passes the same barriers
+  // a general iteration: any step may be masked or invisible for this wave
+  auto general = [&](int s) __attribute__((always_inline)) {
+    sync(s, (s + lead) % SL);
     f32x16 nxt = sc;
-    if (more) {
-      sync_next(s);
-      nxt = qk((s + 1) % STAGES);
-    }
-    if (visible(s)) {
-      if (masked(s)) softmax_pv(MaskT{}, s, s % STAGES, sc);
-      else softmax_pv(NoMaskT{}, s, s % STAGES, sc);
+    if (s + 1 < nsteps) nxt = qk((s + 1) % SL);
+    if (s >= 1 && visible(s - 1)) pv(pw_prev, (s - 1) % SL);
+    if (s < nsteps && visible(s)) {
+      bool resc;
+      const float alpha = masked(s) ? softmax(MaskT{}, s, sc, pw_prev, resc) : softmax(NoMaskT{}, s, sc, pw_prev, resc);
+      if (resc) rescale(alpha);
     }
     sc = nxt;
+  };
+  // iterations [1, n_hot) are hot: steps s-1, s visible and unmasked for
+  // every wave, step s+1 present and the step either wave type loads
+  // (s + SL at most) wholly below kv_end
+  const int n_whole = max(0, min(nsteps, kv_end / BKV - t_begin));
+  const int n_hot = min(min(n_full, nsteps - 1), n_whole - SL);
+  int s = 0;
+  if (nsteps > 0) general(s++);
+  // The DMA of the iteration goes out in two halves between the LDS reads of
+  // the score and P V products: issued in one burst after the barrier, the
+  // loads of all 8 waves queue at the texture unit and stall the waves'
+  // compute behind them.
+  auto hot = [&](int s, int kslot, int vslot, int islot) __attribute__((always_inline)) {
+    wait_barrier(s);
+    const f32x16 nxt = qk(kslot);
+    issue_rows(s + lead, islot, 0, NPW / 2);
+    pv(pw_prev, vslot);
+    issue_rows(s + lead, islot, NPW / 2, NPW);
+    bool resc;
+    const float alpha = softmax(NoMaskT{}, s, sc, pw_prev, resc);
+    if (resc) rescale(alpha);
+    sc = nxt;
+  };
+  // unrolled by SL from s = 1 (mod SL): every slot is a constant (the
+  // addresses fold) and the next-step scores take turns in registers
+  for (; s + SL <= n_hot; s += SL) {
+#pragma unroll
+    for (int u = 0; u < SL; ++u) hot(s + u, (u + 2) % SL, u % SL, isk ? (u + 1) % SL : (u + SL - 1) % SL);
   }
+  for (; s < n_hot; ++s) hot(s, (s + 1) % SL, (s - 1) % SL, (s + lead) % SL);
+  if (nsteps > 0)
+    for (; s <= nsteps; ++s) general(s);
   vm_wait<0>();
   __syncthreads();  // every wave is done with the ring
 
-  // ---- merge the KH partial states of each query in kh order
+  // ---- merge the KH partial states of each query in kh order.  A lane
+  // holds, for its query, 4 consecutive d in each of 16 runs: 16-byte LDS
+  // writes.
   float *part = reinterpret_cast<float *>(ring) + wid * 32 * PS;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      part[(lane & 31) * PS + db * 32 + (i >> 2) * 8 + h * 4 + (i & 3)] = acc_o[db][i];
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<f32x4 *>(part + (lane & 31) * PS + db * 32 + j * 8 + h * 4) =
+          f32x4{acc_o[db][4 * j], acc_o[db][4 * j + 1], acc_o[db][4 * j + 2], acc_o[db][4 * j + 3]};
   if (h == 0) {
     ml_s[wid][lane & 31][0] = m_run;
     ml_s[wid][lane & 31][1] = l_run;
   }
   __syncthreads();
-  constexpr int TPQ = FA_THREADS / BQ;  // threads per query
-  constexpr int DPT = DP / TPQ;         // outputs per thread
-  static_assert(DPT % 8 == 0, "16-byte stores");
-  const int ql = tid / TPQ, seg = tid % TPQ;
-  const int g2 = ql >> 5, qi = ql & 31;
-  const int q = q0 + ql;
-  if (q >= g.S_q) return;
-  // states are (m, l, o) with o, l relative to 2^(m c): weights 2^((m_k - M) c)
-  float M = -INFINITY;
+  // Outputs: consecutive threads own consecutive 4-float chunks of a query
+  // row, so each store instruction writes whole rows.
+  constexpr int CPR = DP / 4;            // chunks per row
+  constexpr int RPP = FA_THREADS / CPR;  // rows per pass
+  static_assert(BQ % RPP == 0, "whole passes");
+  const int cc = tid % CPR, rr = tid / CPR;
+  const float *mrg = reinterpret_cast<const float *>(ring);
 #pragma unroll
-  for (int k = 0; k < KH; ++k) M = fmaxf(M, ml_s[g2 + QG * k][qi][0]);
-  float wk[KH], L = 0.f;
+  for (int pass = 0; pass < BQ / RPP; ++pass) {
+    const int ql = pass * RPP + rr;
+    const int g2 = ql >> 5, qi = ql & 31;
+    const int q = q0 + ql;
+    if (q >= g.S_q) break;  // later passes hold later queries
+    // states are (m, l, o) with o, l relative to 2^(m c): weights 2^((m_k - M) c)
+    float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < KH; ++k) {
-    const float mk = ml_s[g2 + QG * k][qi][0];
-    wk[k] = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mk - M) * c2);
-    L += ml_s[g2 + QG * k][qi][1] * wk[k];
-  }
-  const size_t orow = (size_t)bh * g.S_q + q;
-  if (g.splits == 1) {
-    const float inv = 1.0f / L;
-    uint32_t o[DPT / 2];
+    for (int k = 0; k < KH; ++k) M = fmaxf(M, ml_s[g2 + QG * k][qi][0]);
+    float wk[KH], L = 0.f;
 #pragma unroll
-    for (int e = 0; e < DPT; e += 2) {
-      float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-      for (int k = 0; k < KH; ++k) {
-        const float *pk = reinterpret_cast<const float *>(ring) + (g2 + QG * k) * 32 * PS + qi * PS + seg * DPT + e;
-        a0 += pk[0] * wk[k];
-        a1 += pk[1] * wk[k];
-      }
-      o[e >> 1] = pack_bf(a0 * inv, a1 * inv);
+    for (int k = 0; k < KH; ++k) {
+      const float mk = ml_s[g2 + QG * k][qi][0];
+      wk[k] = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mk - M) * c2);
+      L += ml_s[g2 + QG * k][qi][1] * wk[k];
     }
-    uint16_t *op = g.O + orow * DP + seg * DPT;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < DPT / 8; ++e)
-      *reinterpret_cast<u32x4 *>(op + 8 * e) = u32x4{o[4 * e], o[4 * e + 1], o[4 * e + 2], o[4 * e + 3]};
-  } else {
-    // this split's state for the query: max Mu, sum L, unnormalised o
-    const size_t prow = (size_t)split * g.BH * g.S_q + orow;
-    float *po = g.part_o + prow * DP + seg * DPT;
-#pragma unroll
-    for (int e = 0; e < DPT; e += 4) {
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k = 0; k < KH; ++k) {
-        const float *pk = reinterpret_cast<const float *>(ring) + (g2 + QG * k) * 32 * PS + qi * PS + seg * DPT + e;
-        v += *reinterpret_cast<const f32x4 *>(pk) * wk[k];
+    for (int k = 0; k < KH; ++k)
+      v += *reinterpret_cast<const f32x4 *>(mrg + (g2 + QG * k) * 32 * PS + qi * PS + 4 * cc) * wk[k];
+    const size_t orow = (size_t)bh * g.S_q + q;
+    if (g.splits == 1) {
+      const float inv = 1.0f / L;
+      *reinterpret_cast<u32x2 *>(g.O + orow * DP + 4 * cc) =
+          u32x2{pack_bf(v[0] * inv, v[1] * inv), pack_bf(v[2] * inv, v[3] * inv)};
+    } else {
+      // this split's state for the query: max M, sum L, unnormalised o
+      const size_t prow = (size_t)split * g.BH * g.S_q + orow;
+      *reinterpret_cast<f32x4 *>(g.part_o + prow * DP + 4 * cc) = v;
+      if (cc == 0) {
+        g.part_ml[prow * 2] = M;
+        g.part_ml[prow * 2 + 1] = L;
       }
-      *reinterpret_cast<f32x4 *>(po + e) = v;
-    }
-    if (seg == 0) {
-      g.part_ml[prow * 2] = M;
-      g.part_ml[prow * 2 + 1] = L;
     }
   }
 }
@@ -779,27 +839,40 @@ int kv_append_inplace_launch(uint16_t *cache, const uint16_t *neu, int64_t BH, i
 
 // The flash-style kernel when the shape suits it: D 64 or 128 and 16-byte
 // aligned tensors (callers also require scale > 0: the kernel tracks the
-// running max on unscaled scores).  With Kn/Vn (fused append) the new rows must start on a
-// 64-key step (S_cache a multiple of 64).
+// running max on unscaled scores).  With Kn/Vn (fused append) the new rows
+// must start on a key step of the tile shape (S_cache a multiple of bkv).
 bool fa_applicable(int S_kv, int S_cache, int D, int kv_rows, const void *Q, const void *K, const void *V,
-                   const void *O, const void *Kn, const void *Vn, const void *Kc, const void *Vc) {
+                   const void *O, const void *Kn, const void *Vn, const void *Kc, const void *Vc, int bkv) {
   if (D != 64 && D != 128) return false;
   if (S_kv <= 0) return false;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return false;
   if ((size_t)kv_rows * D * 2 >= (size_t(1) << 31)) return false;
   if (Kn) {
     if (!aligned16(Kn) || !aligned16(Vn) || !aligned16(Kc) || !aligned16(Vc)) return false;
-    if (S_cache % 64 != 0) return false;  // one source per 64-key step
+    if (S_cache % bkv != 0) return false;  // one source per key step
     if ((size_t)(S_kv - S_cache) * D * 2 >= (size_t(1) << 31)) return false;
   }
   return true;
 }
 
-// Launch the flash-style kernel: 128 queries per workgroup (4 query groups x
-// 2 key halves of a 64-key step) and enough key splits to reach ~256
-// workgroups, each split keeping >= 8 steps.
-int attention_fa(FaArgs a, int D, hipStream_t st) {
-  constexpr int QG = 4, BQ = 128, BKV = 64;
+// The two tile shapes of the flash kernel: QG query groups of 32 and
+// 8 / QG key blocks of 32 per step -- 128 queries x 64 keys (QG 4) or
+// 64 queries x 128 keys (QG 2).
+constexpr int fa_bq(int qg) { return 32 * qg; }
+constexpr int fa_bkv(int qg) { return 32 * (FA_WAVES / qg); }
+
+// Built-in tile shape: 128 x 64 when its query tiles alone fill the chip
+// (256 workgroups); otherwise 64 x 128, which doubles the workgroups without
+// the key splits (and their fp32 partials and merge kernel) that a short
+// grid otherwise needs.
+int fa_default_qg(int64_t BH, int S_q) {
+  return BH * ((S_q + fa_bq(4) - 1) / fa_bq(4)) >= 256 ? 4 : 2;
+}
+
+// Launch the flash-style kernel with QG query groups per workgroup, with
+// enough key splits to reach ~256 workgroups, each split keeping >= 8 steps.
+int attention_fa(FaArgs a, int D, int qg, hipStream_t st) {
+  const int BQ = fa_bq(qg), BKV = fa_bkv(qg);
   a.q_tiles = (a.S_q + BQ - 1) / BQ;
   const int ntiles = (a.S_kv + BKV - 1) / BKV;
   a.splits = 1;
@@ -816,13 +889,19 @@ int attention_fa(FaArgs a, int D, hipStream_t st) {
   }
   const int blocks = a.BH * a.q_tiles * a.splits;
   const bool fused = a.Kn != nullptr;
+#define PK_FA_LAUNCH(DPV, QGV)                                                              \
+  do {                                                                                      \
+    if (fused) attention_fa_kernel<DPV, QGV, true><<<blocks, FA_THREADS, 0, st>>>(a);       \
+    else attention_fa_kernel<DPV, QGV, false><<<blocks, FA_THREADS, 0, st>>>(a);            \
+  } while (0)
   if (D == 128) {
-    if (fused) attention_fa_kernel<128, QG, true><<<blocks, FA_THREADS, 0, st>>>(a);
-    else attention_fa_kernel<128, QG, false><<<blocks, FA_THREADS, 0, st>>>(a);
+    if (qg == 4) PK_FA_LAUNCH(128, 4);
+    else PK_FA_LAUNCH(128, 2);
   } else {
-    if (fused) attention_fa_kernel<64, QG, true><<<blocks, FA_THREADS, 0, st>>>(a);
-    else attention_fa_kernel<64, QG, false><<<blocks, FA_THREADS, 0, st>>>(a);
+    if (qg == 4) PK_FA_LAUNCH(64, 4);
+    else PK_FA_LAUNCH(64, 2);
   }
+#undef PK_FA_LAUNCH
   PK_LAUNCH_CHECK("attention_fa_kernel");
   if (a.splits > 1) {
     const int64_t items = (int64_t)a.BH * a.S_q * (D / 8);
@@ -834,27 +913,69 @@ int attention_fa(FaArgs a, int D, hipStream_t st) {
   return PK_OK;
 }
 
-// The kernel attention runs for aligned operands and scale > 0, as a config:
-// the flash-style kernel for D 64 / 128 (128 queries x 64-key steps, 8 waves,
-// K/V ring of 128 KiB / (2 * 64 * D * 2) steps), the generic one otherwise.
-// unroll = MFMA k-steps of one query-key product.
-bool attention_config(int S_q, int S_kv, int D, pk_config *out) {
-  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 128) return false;
-  if (D == 64 || D == 128) {
-    *out = pk_config{128, 64, D, FA_WAVES, 8, D / 16, FA_RING / (2 * 64 * D * 2)};
-  } else {
-    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : 128;
-    *out = pk_config{AT_BQ, AT_BKV, dp, AT_WAVES, D % 8 == 0 ? 8 : 1, dp / 16, 1};
-  }
+// Configs of attention as descriptors: the flash kernel's two tile shapes
+// for D 64 / 128 ({queries, keys per step, D, 8 waves, 16-byte vectors,
+// D/16 MFMA k-steps per product, K/V ring slots}), the generic kernel
+// otherwise.  unroll = MFMA k-steps of one query-key product.
+pk_config fa_config(int qg, int D) {
+  return pk_config{fa_bq(qg), fa_bkv(qg), D, FA_WAVES, 8, D / 16, FA_RING / (2 * fa_bkv(qg) * D * 2)};
+}
+bool generic_attention_config(int D, pk_config *out) {
+  const int dp = D <= 32 ? 32 : D <= 64 ? 64 : 128;
+  *out = pk_config{AT_BQ, AT_BKV, dp, AT_WAVES, D % 8 == 0 ? 8 : 1, dp / 16, 1};
   return true;
 }
+int attention_configs(int S_q, int S_kv, int D, pk_config *out, int cap) {
+  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 128) return 0;
+  pk_config c[2];
+  int n = 0;
+  if (D == 64 || D == 128) {
+    c[n++] = fa_config(4, D);
+    c[n++] = fa_config(2, D);
+  } else {
+    generic_attention_config(D, &c[n++]);
+  }
+  for (int i = 0; i < n && i < cap; ++i) out[i] = c[i];
+  return n;
+}
+// The built-in choice.  The shape key has no batch x heads: this assumes 32
+// (the headline configuration's and the autotuner's default).
+bool attention_config(int S_q, int S_kv, int D, pk_config *out) {
+  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 128) return false;
+  if (D == 64 || D == 128) *out = fa_config(fa_default_qg(32, S_q), D);
+  else generic_attention_config(D, out);
+  return true;
+}
+// The query groups a flash config names (0: not a flash config for D).
+int fa_qg_of(const pk_config &c, int D) {
+  for (int qg : {4, 2}) {
+    const pk_config f = fa_config(qg, D);
+    if (c.block_m == f.block_m && c.block_n == f.block_n && c.block_k == f.block_k && c.num_warps == f.num_warps &&
+        c.vector_width == f.vector_width && c.unroll == f.unroll && c.shared_memory_stages == f.shared_memory_stages)
+      return qg;
+  }
+  return 0;
+}
 
+// mode 0: the built-in kernel and tile shape; 2 or 4: the flash kernel
+// with that many query groups (an error when it does not apply); -1: the
+// generic kernel.
 int attention_run(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O, int BH,
-                  int S_q, int S_kv, int D, int kv_rows, float scale, int causal, hipStream_t st) {
-  if (scale > 0.f && fa_applicable(S_kv, S_kv, D, kv_rows, Q, K, V, O, nullptr, nullptr, nullptr, nullptr)) {
-    FaArgs a{Q, K, V, nullptr, nullptr, nullptr, nullptr, O, nullptr, nullptr, BH, S_q, S_kv, S_kv, kv_rows,
-             scale, causal, 1, 1};
-    return attention_fa(a, D, st);
+                  int S_q, int S_kv, int D, int kv_rows, float scale, int causal, int mode, hipStream_t st) {
+  if (mode >= 0) {
+    const int qg = mode ? mode : fa_default_qg(BH, S_q);
+    if (scale > 0.f && fa_applicable(S_kv, S_kv, D, kv_rows, Q, K, V, O, nullptr, nullptr, nullptr, nullptr,
+                                     fa_bkv(qg))) {
+      FaArgs a{Q, K, V, nullptr, nullptr, nullptr, nullptr, O, nullptr, nullptr, BH, S_q, S_kv, S_kv, kv_rows,
+               scale, causal, 1, 1};
+      return attention_fa(a, D, qg, st);
+    }
+    if (mode) {
+      set_error("attention: the flash kernel (%d x %d tiles) needs D 64 or 128, 16-byte aligned tensors and "
+                "scale > 0",
+                fa_bq(qg), fa_bkv(qg));
+      return PK_ERR_UNSUPPORTED;
+    }
   }
   AttArgs g{Q, K, V, O, nullptr, nullptr, BH, S_q, S_kv, D, kv_rows, scale, causal, 1, 1};
   if (D <= 32) return attention_dp<32>(g, st);
@@ -862,6 +983,46 @@ int attention_run(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint1
   if (D <= 128) return attention_dp<128>(g, st);
   set_error("attention: head dim %d > 128 is not supported", D);
   return PK_ERR_UNSUPPORTED;
+}
+
+int fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc, const uint16_t *Kn,
+                              const uint16_t *Vn, uint16_t *O, int B, int H, int S_q, int S_cache, int D,
+                              int cache_capacity, float scale, int causal, int mode, hipStream_t st) {
+  PK_CHECK_ARG(Q && Kc && Vc && O && (S_q == 0 || (Kn && Vn)),
+               "launch_fused_kv_append_attention: null tensor pointer");
+  PK_CHECK_ARG(B >= 0 && H >= 0 && S_q >= 0 && S_cache >= 0 && D > 0,
+               "launch_fused_kv_append_attention: invalid shape");
+  PK_CHECK_ARG((int64_t)S_cache + S_q <= cache_capacity,
+               "launch_fused_kv_append_attention: S_cache + S_q = %lld exceeds cache_capacity %d",
+               (long long)S_cache + S_q, cache_capacity);
+  const int64_t BH = (int64_t)B * H;
+  if (BH == 0) return PK_OK;
+  const int S_kv = S_cache + S_q;
+  if (S_q > 0 && BH <= INT32_MAX && scale > 0.f && mode >= 0) {
+    int qg = mode ? mode : fa_default_qg(BH, S_q);
+    auto fits = [&](int g) {
+      return fa_applicable(S_kv, S_cache, D, cache_capacity, Q, Kc, Vc, O, Kn, Vn, Kc, Vc, fa_bkv(g));
+    };
+    if (!mode && qg == 2 && !fits(2)) qg = 4;  // S_cache on a 64-key but not a 128-key step
+    if (fits(qg)) {
+      // the append happens inside the attention kernel
+      FaArgs a{Q, Kc, Vc, Kn, Vn, Kc, Vc, O, nullptr, nullptr, (int)BH, S_q, S_kv, S_cache, cache_capacity,
+               scale, causal, 1, 1};
+      return attention_fa(a, D, qg, st);
+    }
+  }
+  if (mode > 0) {
+    set_error("launch_fused_kv_append_attention: the flash kernel (%d x %d tiles) needs D 64 or 128, 16-byte "
+              "aligned tensors, scale > 0 and S_cache a multiple of %d",
+              fa_bq(mode), fa_bkv(mode), fa_bkv(mode));
+    return PK_ERR_UNSUPPORTED;
+  }
+  int rc = kv_append_inplace_launch(Kc, Kn, BH, S_cache, S_q, D, cache_capacity, st);
+  if (rc) return rc;
+  rc = kv_append_inplace_launch(Vc, Vn, BH, S_cache, S_q, D, cache_capacity, st);
+  if (rc) return rc;
+  if (S_q == 0) return PK_OK;
+  return attention_run(Q, Kc, Vc, O, (int)BH, S_q, S_kv, D, cache_capacity, scale, causal, mode, st);
 }
 
 }  // namespace pk
@@ -877,37 +1038,37 @@ int launch_attention_prefill(const uint16_t *Q, const uint16_t *K, const uint16_
   PK_CHECK_ARG(B >= 0 && H >= 0 && S_q >= 0 && S_kv >= 0 && D > 0,
                "launch_attention_prefill: invalid shape");
   if ((int64_t)B * H * S_q == 0) return PK_OK;
-  return attention_run(Q, K, V, O, B * H, S_q, S_kv, D, S_kv, scale, causal, (hipStream_t)stream);
+  return attention_run(Q, K, V, O, B * H, S_q, S_kv, D, S_kv, scale, causal, 0, (hipStream_t)stream);
 }
 
 int launch_fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc,
                                      const uint16_t *Kn, const uint16_t *Vn, uint16_t *O, int B,
                                      int H, int S_q, int S_cache, int D, int cache_capacity,
                                      float scale, int causal, void *stream) {
-  PK_CHECK_ARG(Q && Kc && Vc && O && (S_q == 0 || (Kn && Vn)),
-               "launch_fused_kv_append_attention: null tensor pointer");
-  PK_CHECK_ARG(B >= 0 && H >= 0 && S_q >= 0 && S_cache >= 0 && D > 0,
-               "launch_fused_kv_append_attention: invalid shape");
-  PK_CHECK_ARG((int64_t)S_cache + S_q <= cache_capacity,
-               "launch_fused_kv_append_attention: S_cache + S_q = %lld exceeds cache_capacity %d",
-               (long long)S_cache + S_q, cache_capacity);
-  hipStream_t st = (hipStream_t)stream;
-  const int64_t BH = (int64_t)B * H;
-  if (BH == 0) return PK_OK;
-  const int S_kv = S_cache + S_q;
-  if (S_q > 0 && BH <= INT32_MAX && scale > 0.f &&
-      fa_applicable(S_kv, S_cache, D, cache_capacity, Q, Kc, Vc, O, Kn, Vn, Kc, Vc)) {
-    // the append happens inside the attention kernel
-    FaArgs a{Q, Kc, Vc, Kn, Vn, Kc, Vc, O, nullptr, nullptr, (int)BH, S_q, S_kv, S_cache, cache_capacity,
-             scale, causal, 1, 1};
-    return attention_fa(a, D, st);
+  return fused_kv_append_attention(Q, Kc, Vc, Kn, Vn, O, B, H, S_q, S_cache, D, cache_capacity, scale, causal, 0,
+                                   (hipStream_t)stream);
+}
+
+int pk_fused_kv_append_attention_config(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc, const uint16_t *Kn,
+                                        const uint16_t *Vn, uint16_t *O, int B, int H, int S_q, int S_cache,
+                                        int D, int cache_capacity, float scale, int causal, const pk_config *cfg,
+                                        void *stream) {
+  int mode = 0;
+  if (cfg) {
+    pk_config gen{};
+    generic_attention_config(D, &gen);
+    mode = fa_qg_of(*cfg, D);
+    if (!mode) {
+      PK_CHECK_ARG(std::memcmp(cfg, &gen, sizeof gen) == 0,
+                   "pk_fused_kv_append_attention_config: {%d, %d, %d, %d, %d, %d, %d} is not a config of the "
+                   "gfx950 attention kernels for D = %d",
+                   cfg->block_m, cfg->block_n, cfg->block_k, cfg->num_warps, cfg->vector_width, cfg->unroll,
+                   cfg->shared_memory_stages, D);
+      mode = -1;
+    }
   }
-  int rc = kv_append_inplace_launch(Kc, Kn, BH, S_cache, S_q, D, cache_capacity, st);
-  if (rc) return rc;
-  rc = kv_append_inplace_launch(Vc, Vn, BH, S_cache, S_q, D, cache_capacity, st);
-  if (rc) return rc;
-  if (S_q == 0) return PK_OK;
-  return attention_run(Q, Kc, Vc, O, (int)BH, S_q, S_cache + S_q, D, cache_capacity, scale, causal, st);
+  return fused_kv_append_attention(Q, Kc, Vc, Kn, Vn, O, B, H, S_q, S_cache, D, cache_capacity, scale, causal,
+                                   mode, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -350,7 +350,7 @@ int pk_op_configs(const char *op, long long M, long long N, long long K, pk_conf
     case OF_RMSNORM_MATMUL: return single(rmsnorm_matmul_config(m, n, k, &c), c, out, cap);
     case OF_RMSNORM: return single(k == 0 && rmsnorm_config(m, n, &c), c, out, cap);
     case OF_SOFTMAX: return single(k == 0 && softmax_config(m, n, &c), c, out, cap);
-    case OF_ATTENTION: return single(n >= m && attention_config(m, n, k, &c), c, out, cap);
+    case OF_ATTENTION: return n >= m ? attention_configs(m, n, k, out, cap) : 0;
     default: return 0;
   }
 }

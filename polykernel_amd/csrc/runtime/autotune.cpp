@@ -323,8 +323,9 @@ bool PrepareAttention(const Shape &s, const AutotuneOptions &o, DeviceArena &are
   w.golden = [=](hipStream_t st) {
     return pk_naive_attention(Q, Kc[0], Vc[0], want, heads, Sq, Skv, Skv, D, scale, 1, st);
   };
-  w.run = [=](const pk_config *, int c, hipStream_t st) {
-    return launch_fused_kv_append_attention(Q, Kc[c], Vc[c], Kn, Vn, w.out[c], 1, BH, Sq, Sc, D, Skv, scale, 1, st);
+  w.run = [=](const pk_config *cfg, int c, hipStream_t st) {
+    return pk_fused_kv_append_attention_config(Q, Kc[c], Vc[c], Kn, Vn, w.out[c], 1, BH, Sq, Sc, D, Skv, scale, 1,
+                                               cfg, st);
   };
   return true;
 }

@@ -215,9 +215,10 @@ void RegisterBuiltinLaunchers(Runtime &rt) {
   rt.RegisterLauncher("fused_kv_append_attention", [](const CacheEntry &e, void *io, std::string &error) {
     KvAppendAttentionIO *p = Cast<KvAppendAttentionIO>(io, error);
     if (!p || !CheckEntry(e, p->S_q, (std::int64_t)p->S_cache + p->S_q, p->D, error)) return false;
-    return Launched(launch_fused_kv_append_attention(p->Q, p->Kc, p->Vc, p->Kn, p->Vn, p->O, p->B, p->H, p->S_q,
-                                                     p->S_cache, p->D, p->cache_capacity, p->scale, p->causal,
-                                                     p->stream),
+    const pk_config cfg = ToPk(e.best);
+    return Launched(pk_fused_kv_append_attention_config(p->Q, p->Kc, p->Vc, p->Kn, p->Vn, p->O, p->B, p->H, p->S_q,
+                                                        p->S_cache, p->D, p->cache_capacity, p->scale, p->causal,
+                                                        &cfg, p->stream),
                     e, error);
   });
 }

@@ -538,6 +538,82 @@ def test_fused_kv_append_attention_config3_heads(gpu, oracle):
                           True) == 0, rep
 
 
+@pytest.mark.parametrize("Sc,Sn,D", [(256, 160, 128), (384, 100, 64)])
+def test_fused_kv_append_attention_every_config(gpu, oracle, Sc, Sn, D):
+    """Each configuration pk_op_configs lists (the flash kernel's 128 x 64 and
+    64 x 128 tile shapes) through pk_fused_kv_append_attention_config: the
+    appended cache bit-exact, outputs within the attention error model."""
+    import ctypes
+
+    import torch
+
+    from polykernel_amd import _lib
+
+    lib = _lib.load()
+    B, H = 1, 4
+    cfgs = (_lib.Config * 8)()
+    n = lib.pk_op_configs(b"fused_kv_append_attention", Sn, Sc + Sn, D, cfgs, 8)
+    assert n == 2, n
+    assert {(cfgs[i].block_m, cfgs[i].block_n) for i in range(n)} == {(128, 64), (64, 128)}
+    q = rng_bf16((B, H, Sn, D), 110)
+    kn, vn = rng_bf16((B, H, Sn, D), 111), rng_bf16((B, H, Sn, D), 112)
+    kc, vc = rng_bf16((B, H, Sc, D), 113), rng_bf16((B, H, Sc, D), 114)
+    kfull, vfull = oracle.kv_append(kc, kn), oracle.kv_append(vc, vn)
+    want = oracle.attention_prefill(q, kfull, vfull, None, True)
+    dq, dkn, dvn = to_dev(q), to_dev(kn), to_dev(vn)
+    st = torch.cuda.current_stream().cuda_stream
+    for i in range(n):
+        c = cfgs[i]
+        _say(f"fused append config {c.block_m}x{c.block_n} Sc={Sc} Sn={Sn} D={D}")
+        kcd = torch.zeros(B, H, Sc + Sn, D, dtype=torch.bfloat16, device="cuda")
+        vcd = torch.zeros_like(kcd)
+        kcd[:, :, :Sc] = to_dev(kc)
+        vcd[:, :, :Sc] = to_dev(vc)
+        out = torch.empty(B, H, Sn, D, dtype=torch.bfloat16, device="cuda")
+        _lib.check(lib.pk_fused_kv_append_attention_config(
+            dq.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), dkn.data_ptr(), dvn.data_ptr(), out.data_ptr(),
+            B, H, Sn, Sc, D, Sc + Sn, 1.0 / np.sqrt(D), 1, ctypes.byref(c), st), "attention config")
+        got = from_dev(out)
+        assert np.array_equal(from_dev(kcd), kfull) and np.array_equal(from_dev(vcd), vfull)
+        rep = mt.report(got, want)
+        _say(f"  {rep}")
+        assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+        assert _att_bound_bad(oracle, got, want, q, kfull, vfull, True) == 0, rep
+
+
+def test_fused_kv_append_attention_config_errors(gpu):
+    """A config outside the list is refused; the 64 x 128 tile shape refuses
+    an S_cache that is not a multiple of its 128-key step (no launch)."""
+    import ctypes
+
+    import torch
+
+    from polykernel_amd import _lib
+
+    lib = _lib.load()
+    B, H, Sn, Sc, D = 1, 2, 64, 192, 128
+    t = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device="cuda")
+    q, kn, vn, out = t(B, H, Sn, D), t(B, H, Sn, D), t(B, H, Sn, D), t(B, H, Sn, D)
+    kc, vc = t(B, H, Sc + Sn, D), t(B, H, Sc + Sn, D)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(c):
+        return lib.pk_fused_kv_append_attention_config(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kn.data_ptr(),
+                                                       vn.data_ptr(), out.data_ptr(), B, H, Sn, Sc, D, Sc + Sn,
+                                                       0.088, 1, ctypes.byref(c), st)
+
+    assert run(_lib.Config(96, 64, 128, 8, 8, 8, 4)) == _lib.PK_ERR_INVALID_ARG
+    assert "not a config" in _lib.last_error()
+    cfgs = (_lib.Config * 8)()
+    n = lib.pk_op_configs(b"fused_kv_append_attention", Sn, Sc + Sn, D, cfgs, 8)
+    wide = [cfgs[i] for i in range(n) if cfgs[i].block_n == 128][0]
+    assert run(wide) == _lib.PK_ERR_UNSUPPORTED
+    assert "multiple of 128" in _lib.last_error()
+    narrow = [cfgs[i] for i in range(n) if cfgs[i].block_n == 64][0]
+    assert run(narrow) == 0
+    torch.cuda.synchronize()
+
+
 # ------------------------------------------------------------------ error paths
 
 def test_invalid_arguments_return_status(gpu):
