@@ -582,11 +582,11 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     }
     return alpha;
   };
-  // O^T += V^T (P_hi + P_lo)^T for one step's V tile
-  auto pv = [&](const Pw &pw, int slot) __attribute__((always_inline)) {
+  // O^T += V^T (P_hi + P_lo)^T for one step's V tile (16-key halves [st0, st1))
+  auto pv = [&](const Pw &pw, int slot, int st0 = 0, int st1 = 2) __attribute__((always_inline)) {
     const uint8_t *vs = ring + (SL + slot) * TB;
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int st = st0; st < st1; ++st) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         i16x4 hv[2];
@@ -681,18 +681,21 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
   const int n_hot = min(min(n_full, nsteps - 1), n_whole - SL);
   int s = 0;
   if (nsteps > 0) general(s++);
-  // The DMA of the iteration goes out in two halves between the LDS reads of
-  // the score and P V products: issued in one burst after the barrier, the
-  // loads of all 8 waves queue at the texture unit and stall the waves'
-  // compute behind them.
+  // The DMA of the iteration goes out in four parts between the LDS reads of
+  // the score and P V products and the softmax: issued in one burst after
+  // the barrier, the loads of all 8 waves queue at the texture unit and
+  // stall the waves' compute behind them.
   auto hot = [&](int s, int kslot, int vslot, int islot) __attribute__((always_inline)) {
     wait_barrier(s);
     const f32x16 nxt = qk(kslot);
-    issue_rows(s + lead, islot, 0, NPW / 2);
-    pv(pw_prev, vslot);
-    issue_rows(s + lead, islot, NPW / 2, NPW);
+    issue_rows(s + lead, islot, 0, NPW / 4);
+    pv(pw_prev, vslot, 0, 1);
+    issue_rows(s + lead, islot, NPW / 4, NPW / 2);
+    pv(pw_prev, vslot, 1, 2);
+    issue_rows(s + lead, islot, NPW / 2, 3 * NPW / 4);
     bool resc;
     const float alpha = softmax(NoMaskT{}, s, sc, pw_prev, resc);
+    issue_rows(s + lead, islot, 3 * NPW / 4, NPW);
     if (resc) rescale(alpha);
     sc = nxt;
   };
