@@ -456,15 +456,17 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
   const uint16_t *src_n = FUSED ? (isk ? g.Kn : g.Vn) + (size_t)bh * S_new * DP : src_c;
   const pk_u32x4 rs_c = rsrc_words(src_c, (uint32_t)((size_t)g.kv_rows * DP * 2));
   const pk_u32x4 rs_n = rsrc_words(src_n, FUSED ? (uint32_t)((size_t)S_new * DP * 2) : 0u);
-  uint32_t voff0[NPW];
-  int lrow[NPW];
+  // Lane offset of instruction j: row (wq*NPW + j)*RPI + lane/CH, swizzled
+  // chunk lc.  RPI rows are 1 KiB and the swizzles see row & 7 (K) or
+  // row & 3 (V), so the offset is vb[j & 1] + 1024*j (the 1024*j goes into
+  // the scalar offset): two registers instead of NPW.
+  static_assert(RPI * DP * 2 == 1024 && NPW % 2 == 0, "DMA row blocks");
+  uint32_t vb[2];
 #pragma unroll
-  for (int j = 0; j < NPW; ++j) {
-    const int qq = wq * NPW + j;
-    const int row = qq * RPI + lane / CH, sl = lane % CH;
+  for (int p = 0; p < 2; ++p) {
+    const int row = (wq * NPW + p) * RPI + lane / CH, sl = lane % CH;
     const int lc = isk ? swz_k<CH>(sl, row) : (sl ^ swz_v<DP>(row));
-    lrow[j] = row;
-    voff0[j] = (uint32_t)(row * DP * 2 + 16 * lc);
+    vb[p] = (uint32_t)(row * DP * 2 + 16 * lc - 1024 * p);
   }
   auto issue = [&](int step, int slot) __attribute__((always_inline)) {
     const int k0 = (t_begin + step) * BKV;
@@ -475,13 +477,14 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     if (k0 + BKV <= kv_end) {
 #pragma unroll
       for (int j = 0; j < NPW; ++j)
-        dma_lds16(rs, tile + (wq * NPW + j) * 1024, voff0[j], (uint32_t)(r0 * DP * 2));
+        dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j & 1], (uint32_t)(r0 * DP * 2 + 1024 * j));
     } else {
 #pragma unroll
       for (int j = 0; j < NPW; ++j) {
-        const int over = max(0, k0 + lrow[j] - (kv_end - 1));  // rows past the last visible one
-        dma_lds16(rs, tile + (wq * NPW + j) * 1024, voff0[j] - (uint32_t)(over * DP * 2),
-                  (uint32_t)(r0 * DP * 2));
+        const int row = (wq * NPW + j) * RPI + lane / CH;
+        const int over = max(0, k0 + row - (kv_end - 1));  // rows past the last visible one
+        dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j & 1] - (uint32_t)(over * DP * 2),
+                  (uint32_t)(r0 * DP * 2 + 1024 * j));
       }
     }
   };
@@ -493,7 +496,8 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     const int r0 = nw ? k0 - S_cache : k0;
     uint8_t *tile = ring + (isk ? slot : SL + slot) * TB;
 #pragma unroll
-    for (int j = j0; j < j1; ++j) dma_lds16(rs, tile + (wq * NPW + j) * 1024, voff0[j], (uint32_t)(r0 * DP * 2));
+    for (int j = j0; j < j1; ++j)
+      dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j & 1], (uint32_t)(r0 * DP * 2 + 1024 * j));
   };
 
   f32x16 acc_o[DB];
