@@ -135,7 +135,10 @@ def bench_mlp(steps: int, warmup: int):
 
 
 def bench_extra(reps: int = 20):
-    """Other BASELINE configs: one timing each (HIP events, warm)."""
+    """Other BASELINE configs after 3 warmup launches: the mean per launch of
+    `reps` back-to-back launches (HIP events around the batch), and the median
+    and minimum of `reps` launches timed one by one; config 1 also cold (a
+    1 GiB buffer written between launches, each launch timed alone)."""
     import numpy as np
     import torch
 
@@ -148,9 +151,27 @@ def bench_extra(reps: int = 20):
     sp = stream.cuda_stream
     out = {}
 
-    def timeit(fn, n=reps, warm=3):
+    stats = {}
+
+    def timeit(fn, n=reps, warm=3, key=None, flush=None):
+        """Mean per launch over n back-to-back launches (per-launch pairs of
+        events when `flush` runs between launches); with `key`, the median and
+        minimum of n launches timed one by one go into stats[key]."""
         for _ in range(warm):
             fn()
+        evs = [event_pair() for _ in range(n)]
+        for e0, e1 in evs:
+            if flush is not None:
+                flush()
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        t = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+        if key:
+            stats[key] = {"median_us": round(t[n // 2] * 1e3, 2), "min_us": round(t[0] * 1e3, 2)}
+        if flush is not None:
+            return sum(t) / n
         e0, e1 = event_pair()
         e0.record(stream)
         for _ in range(n):
@@ -164,12 +185,16 @@ def bench_extra(reps: int = 20):
     g = dev_bf16(synth.normal_bf16((768,), 12, 0.1, 1.0))
     w = dev_bf16(synth.normal_bf16((768, 3072), 13, 1 / math.sqrt(768)))
     o = torch.empty(128, 3072, dtype=torch.bfloat16, device="cuda")
-    ms = timeit(lambda: check(lib.launch_fused_rmsnorm_matmul_gamma(
-        x.data_ptr(), g.data_ptr(), w.data_ptr(), o.data_ptr(), 128, 3072, 768, 1e-6, sp), "cfg1"))
+    cfg1 = lambda: check(lib.launch_fused_rmsnorm_matmul_gamma(
+        x.data_ptr(), g.data_ptr(), w.data_ptr(), o.data_ptr(), 128, 3072, 768, 1e-6, sp), "cfg1")
+    ms = timeit(cfg1, key="warm")
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    ms_cold = timeit(cfg1, key="cold", flush=lambda: big.fill_(1))
     out["rmsnorm_matmul_cfg1"] = {"us": round(ms * 1e3, 2),
                                   "tflops": round(2 * 128 * 3072 * 768 / (ms * 1e-3) / 1e12, 2),
-                                  "note": "warm, L2/MALL-resident (5.7 MB)"}
-    del x, g, w, o
+                                  "warm": stats["warm"], "cold_us": round(ms_cold * 1e3, 2), "cold": stats["cold"],
+                                  "note": "warm: L2/MALL-resident (5.7 MB); cold: a 1 GiB buffer written between launches"}
+    del x, g, w, o, big
 
     # config 3: KV append (in place) + causal prefill, B1 H32 D128, 3584 + 512
     B, H, Sc, Sn, Dh = 1, 32, 3584, 512, 128
@@ -183,11 +208,11 @@ def bench_extra(reps: int = 20):
     o = torch.empty_like(q)
     ms = timeit(lambda: check(lib.launch_fused_kv_append_attention(
         q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kn.data_ptr(), vn.data_ptr(), o.data_ptr(),
-        B, H, Sn, Sc, Dh, Sc + Sn, 1 / math.sqrt(Dh), 1, sp), "cfg3"))
+        B, H, Sn, Sc, Dh, Sc + Sn, 1 / math.sqrt(Dh), 1, sp), "cfg3"), key="cfg3")
     flop = 32216449024
     tf = flop / (ms * 1e-3) / 1e12
     out["attention_prefill_cfg3"] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                                     "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4)}
+                                     "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4), **stats["cfg3"]}
     del q, kn, vn, kc, vc, o
 
     # config 4a: residual + RMSNorm [16384, 8192]
@@ -197,10 +222,10 @@ def bench_extra(reps: int = 20):
     ga = dev_bf16(synth.normal_bf16((C,), 33, 0.1, 1.0))
     oa = torch.empty_like(xa)
     ms = timeit(lambda: check(lib.launch_fused_residual_rmsnorm(
-        xa.data_ptr(), ra.data_ptr(), ga.data_ptr(), oa.data_ptr(), R, C, 1e-6, sp), "cfg4a"))
+        xa.data_ptr(), ra.data_ptr(), ga.data_ptr(), oa.data_ptr(), R, C, 1e-6, sp), "cfg4a"), key="cfg4a")
     gbs = 805322752 / (ms * 1e-3) / 1e9
     out["residual_rmsnorm_cfg4a"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
-                                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+                                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), **stats["cfg4a"]}
     del xa, ra, ga, oa
 
     # config 4b: masked softmax fp32 logits [16384, 8192] + bf16 additive mask
@@ -208,10 +233,10 @@ def bench_extra(reps: int = 20):
     mk = dev_bf16(synth.mask_bf16((R, C), 35, 0.1))
     om = torch.empty(R, C, dtype=torch.bfloat16, device="cuda")
     ms = timeit(lambda: check(lib.launch_fused_softmax_mask(lg.data_ptr(), mk.data_ptr(), om.data_ptr(),
-                                                            R, C, sp), "cfg4b"))
+                                                            R, C, sp), "cfg4b"), key="cfg4b")
     gbs = 1073741824 / (ms * 1e-3) / 1e9
     out["masked_softmax_cfg4b"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
-                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), **stats["cfg4b"]}
     del lg, mk, om
 
     # config 5: int8 decode MLP, M=16, 8192 <-> 28672 (weights quantised on the GPU)
@@ -253,10 +278,10 @@ def bench_extra(reps: int = 20):
         served.run("matmul_int8_gelu", Md, Fd, dd, i1)
         served.run("matmul_int8_residual", Md, dd, Fd, i2)
 
-    ms = timeit(decode_served)
+    ms = timeit(decode_served, key="cfg5")
     gbs = 470433792 / (ms * 1e-3) / 1e9
     out["int8_decode_mlp_cfg5"] = {
-        "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+        "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), **stats["cfg5"],
         "launch_decode_mlp_int8_us": round(ms_entry * 1e3, 2),
         "served_configs": [served.resolve("matmul_int8_gelu", Md, Fd, dd)["best"],
                            served.resolve("matmul_int8_residual", Md, dd, Fd)["best"]],
@@ -289,6 +314,25 @@ def cpu_baseline(inputs, budget_s: float = 12.0):
     return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"{rows} of {M} rows of the config-2 MLP block (rows are independent) in "
                       f"{dt:.1f}s; oracle/oracle.c -O2 -ffp-contract=off, OpenMP over rows"}
+
+
+def cpu_baseline_single(inputs, rows: int = 16):
+    """The same oracle on one thread (the reference's own CPU path is
+    single-threaded): a 16-row sample of config 2, extrapolated per row."""
+    from oracle import pyoracle
+
+    threads = pyoracle.num_threads()
+    pyoracle.set_num_threads(1)
+    try:
+        t0 = time.perf_counter()
+        pyoracle.mlp_block(inputs["x"][:rows], inputs["g"], inputs["w1"], inputs["b1"], inputs["w2"],
+                           inputs["b2"], 1e-6)
+        dt = time.perf_counter() - t0
+    finally:
+        pyoracle.set_num_threads(threads)
+    flop = rows * 2 * (D * F + F * D)
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} of {M} rows of the config-2 MLP block in {dt:.1f}s, one thread"}
 
 
 def read_traffic():
@@ -368,6 +412,8 @@ def main() -> int:
     if not args.no_cpu:
         cpu = cpu_baseline(inputs)
         log(f"cpu baseline: {cpu}")
+        extra["cpu_baseline_single_thread"] = cpu_baseline_single(inputs)
+        log(f"cpu baseline, one thread: {extra['cpu_baseline_single_thread']}")
     line = {
         "metric": METRIC,
         "value": round(value, 2),
