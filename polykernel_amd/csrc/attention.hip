@@ -75,12 +75,16 @@ __device__ __forceinline__ int swz_v(int k) {
   }
 }
 
-// K rows: XOR the chunk index with the row inside aligned groups of 8 chunks
-// (4 when a row has only 4 chunks) for conflict-free ds_read_b128.
+// K rows: XOR the chunk index with row bits so the 16 consecutive rows one
+// ds_read_b128 group reads (16 lanes = 256 B of the 64 x 4-byte banks) hit
+// distinct banks: 256-byte rows (16 chunks) take row & 15; 128-byte rows
+// (8 chunks) split by row parity into bank halves and take (row >> 1) & 7;
+// 64-byte rows take (row >> 2) & 3.
 template <int CH>
 __device__ __forceinline__ int swz_k(int c, int row) {
-  if constexpr (CH >= 8) return (c & ~7) | ((c & 7) ^ (row & 7));
-  else return c ^ (row & 3);
+  if constexpr (CH >= 16) return (c & ~15) | ((c & 15) ^ (row & 15));
+  else if constexpr (CH == 8) return c ^ ((row >> 1) & 7);
+  else return c ^ ((row >> 2) & 3);
 }
 
 template <int DP, bool ALIGNED>
@@ -457,13 +461,14 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
   const pk_u32x4 rs_c = rsrc_words(src_c, (uint32_t)((size_t)g.kv_rows * DP * 2));
   const pk_u32x4 rs_n = rsrc_words(src_n, FUSED ? (uint32_t)((size_t)S_new * DP * 2) : 0u);
   // Lane offset of instruction j: row (wq*NPW + j)*RPI + lane/CH, swizzled
-  // chunk lc.  RPI rows are 1 KiB and the swizzles see row & 7 (K) or
-  // row & 3 (V), so the offset is vb[j & 1] + 1024*j (the 1024*j goes into
-  // the scalar offset): two registers instead of NPW.
-  static_assert(RPI * DP * 2 == 1024 && NPW % 2 == 0, "DMA row blocks");
-  uint32_t vb[2];
+  // chunk lc.  RPI rows are 1 KiB and the swizzles see at most row & 15 (K)
+  // or row & 3 (V), so the offset is vb[j % VP] + 1024*j (the 1024*j goes
+  // into the scalar offset): VP registers instead of NPW.
+  constexpr int VP = RPI >= 16 ? 1 : 16 / RPI > 4 ? 4 : 16 / RPI;
+  static_assert(RPI * DP * 2 == 1024 && NPW % VP == 0, "DMA row blocks");
+  uint32_t vb[VP];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
+  for (int p = 0; p < VP; ++p) {
     const int row = (wq * NPW + p) * RPI + lane / CH, sl = lane % CH;
     const int lc = isk ? swz_k<CH>(sl, row) : (sl ^ swz_v<DP>(row));
     vb[p] = (uint32_t)(row * DP * 2 + 16 * lc - 1024 * p);
@@ -477,13 +482,13 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     if (k0 + BKV <= kv_end) {
 #pragma unroll
       for (int j = 0; j < NPW; ++j)
-        dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j & 1], (uint32_t)(r0 * DP * 2 + 1024 * j));
+        dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j % VP], (uint32_t)(r0 * DP * 2 + 1024 * j));
     } else {
 #pragma unroll
       for (int j = 0; j < NPW; ++j) {
         const int row = (wq * NPW + j) * RPI + lane / CH;
         const int over = max(0, k0 + row - (kv_end - 1));  // rows past the last visible one
-        dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j & 1] - (uint32_t)(over * DP * 2),
+        dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j % VP] - (uint32_t)(over * DP * 2),
                   (uint32_t)(r0 * DP * 2 + 1024 * j));
       }
     }
@@ -497,7 +502,7 @@ __global__ __launch_bounds__(FA_THREADS, 1) void attention_fa_kernel(FaArgs g) {
     uint8_t *tile = ring + (isk ? slot : SL + slot) * TB;
 #pragma unroll
     for (int j = j0; j < j1; ++j)
-      dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j & 1], (uint32_t)(r0 * DP * 2 + 1024 * j));
+      dma_lds16(rs, tile + (wq * NPW + j) * 1024, vb[j % VP], (uint32_t)(r0 * DP * 2 + 1024 * j));
   };
 
   f32x16 acc_o[DB];

@@ -5,8 +5,8 @@
 // v_mfma_f32_32x32x16_bf16.  Per workgroup a BM x BN tile; WM x WN waves, each
 // owning a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks.  A and B k-tiles of
 // 64 are staged through LDS, double-buffered with one barrier per k-tile:
-//   - A rows (128 B) are stored with 16-byte chunks XOR-swizzled by (row & 7),
-//     read as one ds_read_b128 per MFMA A-operand;
+//   - A rows (128 B) are stored with 16-byte chunks XOR-swizzled by
+//     (row >> 1) & 7, read as one ds_read_b128 per MFMA A-operand;
 //   - B rows keep the global N-contiguous order (16-byte chunks swizzled by
 //     k), and the MFMA B-operand (8 consecutive k of one column) is assembled
 //     by two ds_read_b64_tr_b16 transpose reads, so no pre-packed weights and
@@ -59,6 +59,12 @@ __device__ __forceinline__ int swz_b(int k) {
     return (k & 3) * 2;
   }
 }
+
+// LDS: 64 banks of 4 bytes; a ds_read_b128 is served 16 lanes (256 B) at a
+// time.  A operand rows of 128 B: the 16 rows one group reads span two bank
+// halves by row parity, and XOR-ing the chunk with (row >> 1) & 7 spreads the 8
+// rows of each parity over all 8 chunk positions (row & 7 gave only 4).
+__device__ __forceinline__ int swz_a64(int row) { return (row >> 1) & 7; }
 
 __device__ __forceinline__ bf16x8 lds_read_a(const uint16_t *p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
@@ -198,7 +204,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < AC; ++i) {
       const int q = tid + i * NT, row = q >> 3, c = q & 7;
-      *reinterpret_cast<u32x4 *>(&As[s][row * BK + ((c ^ (row & 7)) << 3)]) = ra[i];
+      *reinterpret_cast<u32x4 *>(&As[s][row * BK + ((c ^ swz_a64(row)) << 3)]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < BC; ++i) {
@@ -238,7 +244,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
       for (int fm = 0; fm < FM; ++fm) {
         const int row = a_row0 + fm * 32;
         const int c = 2 * s + a_half;
-        af[fm] = lds_read_a(as + row * BK + ((c ^ (row & 7)) << 3));
+        af[fm] = lds_read_a(as + row * BK + ((c ^ swz_a64(row)) << 3));
       }
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) {
@@ -301,7 +307,11 @@ constexpr int G2_BM = 256, G2_BN = 256, G2_BK = 32, G2_STAGES = 4;
 constexpr int G2_THREADS = 256;
 constexpr int G2_DMA_PER_TILE = 8;  // 1 KiB global_load_lds per wave per tile: 4 for A, 4 for B
 
-__device__ __forceinline__ int swz_a32(int row) { return (row >> 1) & 3; }
+// A rows of 64 B (the DMA kernel's 32-wide k-tiles): the 16 rows of a read
+// group fall 4 to each 64-byte quarter of the banks by row & 3, and
+// (row >> 2) & 3 gives those 4 rows distinct chunks (conflict-free; (row >> 1)
+// & 3 left 2-way conflicts).
+__device__ __forceinline__ int swz_a32(int row) { return (row >> 2) & 3; }
 
 template <int EPI, int STAGES>
 __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
