@@ -152,25 +152,70 @@ __device__ __forceinline__ uint32_t gelu_pair_special(uint32_t w) {
   return ((w & 0x7FFF7FFFu) + 0x00800080u) & 0x80008000u;
 }
 
+// The packed operations of gelu_pair_common as instructions: written as
+// vector-of-u16 C, the compiler turns the min/xor/sub and arithmetic-shift
+// masks into per-half compares and selects (~32 instructions per pair of
+// codes); pinned, the pair takes ~24.  Inline constants of packed ops fill only
+// the low half, so op_sel_hi selects the low half for both lanes.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ uint32_t pk_vsub_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_sub_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vadd_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_add_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vadd_u16v(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_add_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vmin_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vmin1_u16(uint32_t a) {
+  uint32_t r;
+  asm("v_pk_min_u16 %0, %1, 1 op_sel_hi:[1,0]" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vsub1_u16(uint32_t a) {
+  uint32_t r;
+  asm("v_pk_sub_u16 %0, %1, 1 op_sel_hi:[1,0]" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vasr15_i16(uint32_t a) {
+  uint32_t r;
+  asm("v_pk_ashrrev_i16 %0, 15, %1 op_sel_hi:[0,1]" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vbfi(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
+#pragma clang diagnostic pop
 __device__ __forceinline__ uint32_t gelu_pair_common(uint32_t w, const uint16_t *__restrict__ tab) {
-  typedef pk_u16x2 u2;
-  const u2 mag = __builtin_bit_cast(u2, w & 0x7FFF7FFFu);
-  const uint32_t sgn = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_i16x2, w) >> (pk_i16x2){15, 15});
-  const u2 sg = __builtin_bit_cast(u2, sgn);
-  const u2 off = mag - (u2){(unsigned short)GELU_TLO, (unsigned short)GELU_TLO};
-  const u2 lim = (u2){(unsigned short)(GELU_PHI - GELU_TLO), (unsigned short)(GELU_PHI - GELU_TLO)} +
-                 (sg & (u2){(unsigned short)(GELU_NHI - GELU_PHI), (unsigned short)(GELU_NHI - GELU_PHI)});
-  const u2 idx0 = __builtin_elementwise_min(off, lim);
-  // 0xFFFF where off <= lim (the code is in the table), 0 elsewhere
-  const u2 m_tab = __builtin_elementwise_min(off ^ idx0, (u2){1, 1}) - (u2){1, 1};
-  const u2 idx = idx0 + (sg & (u2){(unsigned short)GELU_NPOS, (unsigned short)GELU_NPOS});
-  const uint32_t tv = (uint32_t)tab[idx.x] | ((uint32_t)tab[idx.y] << 16);
+  constexpr uint32_t TLO2 = GELU_TLO | (GELU_TLO << 16);
+  constexpr uint32_t LIM2 = (GELU_PHI - GELU_TLO) | ((GELU_PHI - GELU_TLO) << 16);
+  constexpr uint32_t DLIM2 = (GELU_NHI - GELU_PHI) | ((GELU_NHI - GELU_PHI) << 16);
+  constexpr uint32_t NPOS2 = (uint32_t)GELU_NPOS | ((uint32_t)GELU_NPOS << 16);
+  const uint32_t sgn = pk_vasr15_i16(w);                 // 0xFFFF per negative half
+  const uint32_t off = pk_vsub_u16(w & 0x7FFF7FFFu, TLO2);
+  const uint32_t lim = pk_vadd_u16(sgn & DLIM2, LIM2);
+  const uint32_t idx0 = pk_vmin_u16(off, lim);
+  const uint32_t m_tab = pk_vsub1_u16(pk_vmin1_u16(off ^ idx0));  // 0xFFFF where off <= lim
+  const uint32_t idx = pk_vadd_u16v(idx0, sgn & NPOS2);
+  const uint32_t tv = (uint32_t)tab[idx & 0xFFFFu] | ((uint32_t)tab[idx >> 16] << 16);
   const uint32_t half = pack_bf(0.5f * lo_bf(w), 0.5f * hi_bf(w));
-  const uint32_t m_small = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_i16x2, off) >> (pk_i16x2){15, 15});
-  const uint32_t big = (sgn & 0x80008000u) | (~sgn & w);
-  const uint32_t r = (m_small & half) | (~m_small & big);
-  const uint32_t mt = __builtin_bit_cast(uint32_t, m_tab);
-  return (mt & tv) | (~mt & r);
+  const uint32_t m_small = pk_vasr15_i16(off);           // 0xFFFF where |x| < TLO
+  const uint32_t big = pk_vbfi(sgn, 0x80008000u, w);       // above the table: x, or -0
+  return pk_vbfi(m_tab, tv, pk_vbfi(m_small, half, big));
 }
 
 // Both codes of a pair through the exact per-element rules.
