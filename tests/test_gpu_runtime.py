@@ -299,6 +299,52 @@ def test_runtime_serves_gemm_and_refuses_mismatch(gpu, oracle):
     assert "no tuned kernel" in ei.value.message
 
 
+def test_runtime_serves_committed_attention_entry(gpu):
+    """Config 3 through the default runtime (committed gfx950 cache -> tuned
+    tile shape -> pk_fused_kv_append_attention_config): the same appended cache
+    as the library entry point, and the same output bits when the tuned tile
+    shape is the built-in one (another shape sums the key blocks in another
+    order; the parity tests hold every shape to the oracle)."""
+    import math
+
+    import torch
+
+    B, H, Sc, Sn, D = 1, 32, 3584, 512, 128
+    q = to_dev(synth.normal_bf16((B, H, Sn, D), 120))
+    kn, vn = to_dev(synth.normal_bf16((B, H, Sn, D), 121)), to_dev(synth.normal_bf16((B, H, Sn, D), 122))
+    kc0 = synth.normal_bf16((B, H, Sc, D), 123)
+    vc0 = synth.normal_bf16((B, H, Sc, D), 124)
+
+    def caches():
+        kc = torch.zeros(B, H, Sc + Sn, D, dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros_like(kc)
+        kc[:, :, :Sc] = to_dev(kc0)
+        vc[:, :, :Sc] = to_dev(vc0)
+        return kc, vc
+
+    scale = 1.0 / math.sqrt(D)
+    kc, vc = caches()
+    want = _empty_bf16((B, H, Sn, D))
+    _lib.check(_lib.load().launch_fused_kv_append_attention(
+        _ptr(q), _ptr(kc), _ptr(vc), _ptr(kn), _ptr(vn), _ptr(want), B, H, Sn, Sc, D, Sc + Sn, scale, 1, _stream()),
+        "launch_fused_kv_append_attention")
+    served = rt.default_runtime()
+    entry = served.resolve("fused_kv_append_attention", Sn, Sc + Sn, D)
+    assert entry["best"] in rt.candidates("fused_kv_append_attention", Sn, Sc + Sn, D)
+    kc2, vc2 = caches()
+    got = _empty_bf16((B, H, Sn, D))
+    io = rt.KvAppendAttentionIO(Q=_ptr(q), Kc=_ptr(kc2), Vc=_ptr(vc2), Kn=_ptr(kn), Vn=_ptr(vn), O=_ptr(got),
+                                B=B, H=H, S_q=Sn, S_cache=Sc, D=D, cache_capacity=Sc + Sn, scale=scale, causal=1,
+                                stream=_stream())
+    served.run("fused_kv_append_attention", Sn, Sc + Sn, D, io)
+    assert torch.equal(kc2, kc) and torch.equal(vc2, vc)
+    default = rt.default_config("fused_kv_append_attention", Sn, Sc + Sn, D)
+    if entry["best"] == default:
+        assert np.array_equal(from_dev(got), from_dev(want))
+    else:
+        assert np.abs(f32(from_dev(got)) - f32(from_dev(want))).max() < 0.05
+
+
 # ------------------------------------------------------------------ code objects (emitted, hipModuleLoad)
 
 @pytest.mark.parametrize("op,M,N,Kd,epi", [("matmul_int8_gelu", 16, 28672, 8192, 1),
