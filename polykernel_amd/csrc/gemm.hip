@@ -456,15 +456,18 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   using S3 = std::integral_constant<int, 3>;
   using S4 = std::integral_constant<int, 4>;
 
-  // ---- prologue: tiles 0..STAGES-1 in flight (indices past the end are
-  // clamped to the last tile: every k-tile issues the same number of DMA
-  // loads, so each wait below is a compile-time vmcnt), wait for tile 0.
+  // ---- prologue: tiles 0..STAGES-2 and the A half of tile STAGES-1 in
+  // flight (indices past the end are clamped to the last tile: every k-tile
+  // issues the same number of DMA loads, so each wait below is a compile-time
+  // vmcnt), wait for tile 0.
+  using SL = std::integral_constant<int, STAGES - 1>;
   issue(S0{}, 0);
   issue(S1{}, min(1, KT - 1));
   issue(S2{}, min(2, KT - 1));
-  issue(S3{}, min(3, KT - 1));
-  if constexpr (STAGES > 4) issue(S4{}, min(4, KT - 1));
-  vm_wait<(STAGES - 1) * G2_DMA_PER_TILE>();
+  if constexpr (STAGES > 4) issue(S3{}, min(3, KT - 1));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) issue_one(SL{}, min(STAGES - 1, KT - 1), j);
+  vm_wait<(STAGES - 2) * G2_DMA_PER_TILE + 4>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");  // no LDS access moves above the barrier
   __builtin_amdgcn_sched_barrier(0);
@@ -473,17 +476,26 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   read_frag(f0, S0{}, 0);
   // One k-tile on ring stage C (tile t, t % STAGES == C):
   //   16 MFMAs on substep 0, a fragment-read unit of substep 1 after every
-  //   second MFMA;
+  //   second MFMA and a B load of tile t+STAGES-1 (into the stage the last
+  //   barrier released) after every fourth;
   //   wait for this wave's reads of the stage and its DMA of tile t+1, barrier;
-  //   16 MFMAs on substep 1, alternating a DMA load of tile t+STAGES (into the
-  //   stage just released) and a read unit of tile t+1's substep 0.
+  //   16 MFMAs on substep 1, a read unit of tile t+1's substep 0 after every
+  //   second and an A load of tile t+STAGES (into the stage just released)
+  //   after every fourth.
+  // Spreading each tile's 8 loads over both halves of a k-tile instead of
+  // one half evens out the demand on the texture unit (GEMM2 shape -3.5 %).
+  // Every tile's loads still precede all loads of the next tile, so the
+  // vmcnt waits count the same.
   auto body = [&](auto c, int t) {
     constexpr int st = decltype(c)::value;
     using Next = std::integral_constant<int, (st + 1) % STAGES>;
+    using Prev = std::integral_constant<int, (st + STAGES - 1) % STAGES>;
+    const int tp_dma = min(t + STAGES - 1, KT - 1);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       mfma_one(f0, i);
       if ((i & 1) == 0) read_unit(f1, c, 1, i >> 1);
+      if ((i & 3) == 1) issue_one(Prev{}, tp_dma, 4 + (i >> 2));
       __builtin_amdgcn_sched_barrier(0);
     }
     // this wave's reads of stage st are done and its DMA of tile t+1 landed
@@ -497,7 +509,7 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       mfma_one(f1, i);
-      if ((i & 1) == 1) issue_one(c, tn_dma, i >> 1);
+      if ((i & 3) == 1) issue_one(c, tn_dma, i >> 2);
       if ((i & 1) == 0) read_unit(f0, Next{}, 0, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
