@@ -154,9 +154,10 @@ def bench_extra(reps: int = 20):
     stats = {}
 
     def timeit(fn, n=reps, warm=3, key=None, flush=None):
-        """Mean per launch over n back-to-back launches (per-launch pairs of
-        events when `flush` runs between launches); with `key`, the median and
-        minimum of n launches timed one by one go into stats[key]."""
+        """Mean per launch over n back-to-back launches (the median of three
+        such batches; per-launch pairs of events when `flush` runs between
+        launches); with `key`, the median and minimum of n launches timed one
+        by one go into stats[key]."""
         for _ in range(warm):
             fn()
         evs = [event_pair() for _ in range(n)]
@@ -172,13 +173,18 @@ def bench_extra(reps: int = 20):
             stats[key] = {"median_us": round(t[n // 2] * 1e3, 2), "min_us": round(t[0] * 1e3, 2)}
         if flush is not None:
             return sum(t) / n
-        e0, e1 = event_pair()
-        e0.record(stream)
-        for _ in range(n):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n
+        # three batches of n back-to-back launches, the median batch mean: per-launch
+        # times drift by ~10 % over a few ms within one process (clocks, power)
+        means = []
+        for _ in range(3):
+            e0, e1 = event_pair()
+            e0.record(stream)
+            for _ in range(n):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            means.append(e0.elapsed_time(e1) / n)
+        return sorted(means)[1]
 
     # config 1: RMSNorm -> MatMul fragment (cache-resident)
     x = dev_bf16(synth.normal_bf16((128, 768), 11))

@@ -19,6 +19,14 @@ struct alignas(16) U4 {
 
 __device__ __forceinline__ U4 ld16(const void *p) { return *reinterpret_cast<const U4 *>(p); }
 __device__ __forceinline__ void st16(void *p, U4 v) { *reinterpret_cast<U4 *>(p) = v; }
+// 16-byte load of data read exactly once (the rows of x, r, logits, mask):
+// non-temporal, so the stream does not allocate in the caches.  Measured on
+// MI355X: residual+RMSNorm [16384, 8192] 143 -> 123 us, masked softmax
+// 197 -> 169 us (the same hint on the stores made both slower).
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ U4 ld16_once(const void *p) {
+  return __builtin_bit_cast(U4, __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4 *>(p)));
+}
 
 __device__ __forceinline__ void unpack8(U4 v, float (&f)[8]) {
   f[0] = lo_bf(v.x), f[1] = hi_bf(v.x), f[2] = lo_bf(v.y), f[3] = hi_bf(v.y);
@@ -94,10 +102,10 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const uint16_t *__r
   for (int i = 0; i < VPT; ++i) {
     const int c = lane + i * kLanes;
     if (c < nvec) {
-      unpack8(ld16(x + base + (size_t)c * 8), v[i]);
+      unpack8(ld16_once(x + base + (size_t)c * 8), v[i]);
       if constexpr (RESID) {
         float rv[8];
-        unpack8(ld16(r + base + (size_t)c * 8), rv);
+        unpack8(ld16_once(r + base + (size_t)c * 8), rv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[i][e] = bf2f(f2bf(v[i][e] + rv[e]));
       }
@@ -195,12 +203,12 @@ template <int MODE>
 __device__ __forceinline__ void load_z8(const void *in, const uint16_t *mask, size_t off,
                                         float (&z)[8]) {
   if constexpr (MODE == 0) {
-    unpack8(ld16(static_cast<const uint16_t *>(in) + off), z);
+    unpack8(ld16_once(static_cast<const uint16_t *>(in) + off), z);
   } else {
     const float *xf = static_cast<const float *>(in) + off;
-    const U4 a = ld16(xf), b = ld16(xf + 4);
+    const U4 a = ld16_once(xf), b = ld16_once(xf + 4);
     float m[8];
-    unpack8(ld16(mask + off), m);
+    unpack8(ld16_once(mask + off), m);
     const uint32_t raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) z[e] = bf2f(f2bf(bf2f(f2bf(__uint_as_float(raw[e]))) + m[e]));
