@@ -207,7 +207,7 @@ __device__ __forceinline__ void stream_body(const I8sArgs &g) {
   auto issue = [&](auto c, int t) __attribute__((always_inline)) {
     uint8_t *base = ring(c) + wid * STAGE;
 #pragma unroll
-    for (int q = 0; q < NT; ++q) dma_lds16(w_rsrc, base + 1024 * q, w_off[q], t * I8S_KSTEP * g.N);
+    for (int q = 0; q < NT; ++q) dma_lds16<true>(w_rsrc, base + 1024 * q, w_off[q], t * I8S_KSTEP * g.N);
 #pragma unroll
     for (int q = 0; q < 2 * MT; ++q) dma_lds16(a_rsrc, base + W_BYTES + 1024 * q, a_off[q], t * I8S_KSTEP * 2);
   };

@@ -256,6 +256,9 @@ __device__ __forceinline__ pk_u32x4 rsrc_words(const void *base, uint32_t bytes)
 // iteration.  Callers order these loads with vm_wait<N>() themselves.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+// NT: the data is read once (streamed weights), so the load is non-temporal and
+// does not allocate in the caches.
+template <bool NT = false>
 __device__ __forceinline__ void dma_lds16(pk_u32x4 rsrc, const void *lds, uint32_t voff, uint32_t soff) {
   // lds, soff and rsrc are wave-uniform; readfirstlane keeps them in SGPRs
   // (the "s" constraint does not move a VGPR value by itself)
@@ -265,10 +268,16 @@ __device__ __forceinline__ void dma_lds16(pk_u32x4 rsrc, const void *lds, uint32
                        (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[1]),
                        (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[2]),
                        (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[3])};
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(m0), "v"(voff), "s"(rs), "s"(so)
-               : "memory", "m0");
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs), "s"(so)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs), "s"(so)
+                 : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
