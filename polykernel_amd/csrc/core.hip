@@ -38,7 +38,8 @@ int hip_fail(hipError_t e, const char *what) {
 }
 
 // The compact GELU table (pk_common.hpp, gelu_bits): entry i is the bf16 GELU
-// of gelu_table_code(i), evaluated as kernels/cpu/cpu_reference.cpp:46-55 does:
+// of gelu_table_code(i) (or that slot's sentinel), evaluated as
+// kernels/cpu/cpu_reference.cpp:46-55 does:
 // e = (float)erf((double)(x * 0.70710678f)); y = bf16((0.5f * x) * (1.0f + e)).
 __device__ uint16_t g_gelu_table_storage[GELU_TABLE_SIZE];
 
@@ -46,8 +47,14 @@ __global__ void gelu_table_init_kernel(uint16_t *tab) {
 #pragma clang fp contract(off)
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= GELU_TABLE_SIZE) return;
+  bool sentinel;
+  const uint32_t code = gelu_table_code(i, &sentinel);
+  if (sentinel) {
+    tab[i] = (uint16_t)code;
+    return;
+  }
   const float kInvSqrt2 = 0.70710678118654752440f;
-  const float x = bf2f(gelu_table_code(i));
+  const float x = bf2f(code);
   const float e = (float)erf((double)(x * kInvSqrt2));
   const float y = (0.5f * x) * (1.0f + e);
   tab[i] = (uint16_t)f2bf(y);
@@ -66,9 +73,9 @@ __global__ void bf16_selfcheck_kernel(unsigned long long *bad) {
 }
 
 // Self-check of the paired GELU: for every low code (all 65536) and four
-// high-code patterns, gelu_pair_common (where neither code is a NaN or an
-// infinity) and the dispatch the GEMM epilogue uses must equal gelu_bits of
-// each code.
+// high-code patterns, gelu_pair_common (where gelu_pair_special finds neither
+// code outside its domain) and the dispatch the GEMM epilogue uses must equal
+// gelu_bits of each code.
 __global__ void gelu_pair_selfcheck_kernel(const uint16_t *tab, unsigned long long *bad) {
   const uint32_t lo = blockIdx.x * blockDim.x + threadIdx.x;
   if (lo >= 65536u) return;

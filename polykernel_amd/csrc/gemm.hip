@@ -605,10 +605,35 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
         }
       }
       if (__builtin_amdgcn_ballot_w64(special != 0) == 0) {
+        // Table reads one chunk ahead: chunk j+1's indices and reads are
+        // issued before chunk j's results are formed, so each wait covers the
+        // LDS latency of four pairs rather than of one (GEMM1 shape: 482 ->
+        // 472 us; two chunks ahead measured the same).
+        constexpr int G = 1;  // chunks per group (4 pairs each)
+        GeluPairIdx t[2][G][4];
+        uint32_t tl[2][G][4], th[2][G][4];
+        auto fetch = [&](int b, int j0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
+          for (int jj = 0; jj < G; ++jj)
 #pragma unroll
-          for (int w = 0; w < 4; ++w) u[j][w] = gelu_pair_common(u[j][w], tab_lds);
+            for (int w = 0; w < 4; ++w) {
+              t[b][jj][w] = gelu_pair_index(u[j0 + jj][w]);
+              tl[b][jj][w] = tab_lds[t[b][jj][w].idx & 0xFFFFu];
+              th[b][jj][w] = tab_lds[t[b][jj][w].idx >> 16];
+            }
+        };
+        fetch(0, 0);
+#pragma unroll
+        for (int j0 = 0; j0 < 16; j0 += G) {
+          const int b = (j0 / G) & 1;
+          if (j0 + G < 16) fetch(b ^ 1, j0 + G);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int jj = 0; jj < G; ++jj)
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+              u[j0 + jj][w] = gelu_pair_finish(u[j0 + jj][w], t[b][jj][w].off, tl[b][jj][w] | (th[b][jj][w] << 16));
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < 16; ++j)

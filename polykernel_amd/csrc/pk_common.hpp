@@ -104,16 +104,27 @@ __device__ __forceinline__ uint32_t pack_bf(float a, float b) {
 //   |x| < bf16 0x3B4B (~0.0031): bf16(0.5 * x)  (erf's contribution is below
 //       half an ulp);
 //   x > 0x4031 (~2.77): x;  x < -bf16 0x40B1 (~-5.53): -0;
-//   otherwise a table value: codes 0x3B4B..0x4031 and -(0x3B4B..0x40B1),
-//   2638 entries (5 KiB, L1-resident) computed on the device with the
-//   reference formula.
+//   otherwise a table value.
+// Table layout (2768 entries, 5.4 KiB, computed on the device with the
+// reference formula): slots [0, SPAN) hold codes 0x3B4B..0x40B1 (the
+// positive ones above 0x4031 map to themselves), slot SPAN the sentinel
+// 0xFFFF; slots [HALF, HALF + SPAN) hold -(0x3B4B..0x40B1) and slot
+// HALF + SPAN the sentinel 0x8000.  Both signs share one index range, and a
+// clamped index lands on the sentinel, whose unsigned 16-bit min with the
+// input is the "above the table" result (x, or -0): see gelu_pair_common.
 constexpr uint32_t GELU_TLO = 0x3B4Bu, GELU_PHI = 0x4031u, GELU_NHI = 0x40B1u;
-constexpr int GELU_NPOS = (int)(GELU_PHI - GELU_TLO + 1);
-constexpr int GELU_NNEG = (int)(GELU_NHI - GELU_TLO + 1);
-constexpr int GELU_TABLE_SIZE = GELU_NPOS + GELU_NNEG;
+constexpr int GELU_SPAN = (int)(GELU_NHI - GELU_TLO + 1);
+constexpr int GELU_HALF = GELU_SPAN + 1;
+constexpr int GELU_TABLE_SIZE = 2 * GELU_HALF;
 
-__device__ __forceinline__ uint32_t gelu_table_code(int i) {
-  return i < GELU_NPOS ? GELU_TLO + (uint32_t)i : 0x8000u | (GELU_TLO + (uint32_t)(i - GELU_NPOS));
+// The bf16 code of table slot i; a sentinel slot is reported through *sentinel
+// with its stored value as the result.
+__device__ __forceinline__ uint32_t gelu_table_code(int i, bool *sentinel) {
+  const bool neg = i >= GELU_HALF;
+  const int j = neg ? i - GELU_HALF : i;
+  *sentinel = j == GELU_SPAN;
+  if (*sentinel) return neg ? 0x8000u : 0xFFFFu;
+  return (neg ? 0x8000u : 0u) | (GELU_TLO + (uint32_t)j);
 }
 
 // Branch-free: the table is read at a clamped index for every input (always
@@ -122,8 +133,8 @@ __device__ __forceinline__ uint32_t gelu_bits(uint32_t u, const uint16_t *__rest
   const uint32_t mag = u & 0x7FFFu;
   const bool neg = (u & 0x8000u) != 0u;
   const uint32_t off = mag - GELU_TLO;  // wraps for mag < TLO
-  const bool in_tab = off <= (neg ? GELU_NHI - GELU_TLO : GELU_PHI - GELU_TLO);
-  const uint32_t idx = in_tab ? (neg ? (uint32_t)GELU_NPOS : 0u) + off : 0u;
+  const bool in_tab = off < (uint32_t)GELU_SPAN;
+  const uint32_t idx = in_tab ? (neg ? (uint32_t)GELU_HALF : 0u) + off : 0u;
   const uint32_t tv = tab[idx];
   const uint32_t half = f2bf(0.5f * bf2f(u));
   uint32_t r = neg ? 0x8000u : u;        // |x| above the table: x or -0
@@ -134,39 +145,33 @@ __device__ __forceinline__ uint32_t gelu_bits(uint32_t u, const uint16_t *__rest
 }
 
 // Two GELU codes per register (low half = element 0), with 16-bit packed
-// integer ops, for the common case: neither code is a NaN or an infinity.
-// Same results as gelu_bits there:
-//   mag < TLO           -> bf16(0.5 x), the float formula of gelu_bits
-//   table range         -> tab[(neg ? NPOS : 0) + mag - TLO]
-//   above it            -> x (positive) or -0 (negative)
-// 15-bit magnitudes make "a < b" the sign bit of the packed difference; the
-// table index is clamped into range with a packed min, so every lookup is in
-// bounds, and the selects are bit-field inserts of both halves at once.
+// integer ops, for the common case: neither code is a NaN or an infinity and
+// each magnitude is 0 or >= 0x0100 (exponent field >= 2).  Same results as
+// gelu_bits there:
+//   mag < TLO      -> bf16(0.5 x) = x with the exponent field lowered by one
+//                     (exact for exponent fields >= 2), or the zero itself
+//   table range    -> tab[(neg ? HALF : 0) + mag - TLO]
+//   above it       -> the index clamps to the sentinel (0xFFFF positive,
+//                     0x8000 negative) and min(sentinel, x) is x or -0
+// Every table value v satisfies v <= x as unsigned 16-bit codes (|GELU(x)| <=
+// |x| with the sign of x, or +0), so min(tab[idx], x) is the table value
+// inside the range as well.  15-bit magnitudes make "a < b" the sign bit of
+// the packed difference; every lookup is in bounds; the select is one
+// bit-field insert of both halves.
 typedef unsigned short pk_u16x2 __attribute__((ext_vector_type(2)));
 typedef short pk_i16x2 __attribute__((ext_vector_type(2)));
 
-// Nonzero when either code of the pair is a NaN or an infinity (magnitude
-// >= 0x7F80): mag + 0x80 reaches bit 15 of its half exactly then, and no
-// carry crosses from the low half into the high one.
-__device__ __forceinline__ uint32_t gelu_pair_special(uint32_t w) {
-  return ((w & 0x7FFF7FFFu) + 0x00800080u) & 0x80008000u;
-}
-
 // The packed operations of gelu_pair_common as instructions: written as
-// vector-of-u16 C, the compiler turns the min/xor/sub and arithmetic-shift
-// masks into per-half compares and selects (~32 instructions per pair of
-// codes); pinned, the pair takes ~24.  Inline constants of packed ops fill only
-// the low half, so op_sel_hi selects the low half for both lanes.
+// vector-of-u16 C, the compiler turns the min/sub and arithmetic-shift masks
+// into per-half compares and selects; pinned, each is one instruction for both
+// halves (the pair takes 15 VALU instructions and two LDS reads).  Inline
+// constants of packed ops fill only the low half, so op_sel_hi selects the low
+// half for both lanes.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ uint32_t pk_vsub_u16(uint32_t a, uint32_t b) {
   uint32_t r;
   asm("v_pk_sub_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
-  return r;
-}
-__device__ __forceinline__ uint32_t pk_vadd_u16(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_pk_add_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
   return r;
 }
 __device__ __forceinline__ uint32_t pk_vadd_u16v(uint32_t a, uint32_t b) {
@@ -179,14 +184,19 @@ __device__ __forceinline__ uint32_t pk_vmin_u16(uint32_t a, uint32_t b) {
   asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
-__device__ __forceinline__ uint32_t pk_vmin1_u16(uint32_t a) {
+__device__ __forceinline__ uint32_t pk_vmin_u16s(uint32_t a, uint32_t b) {
   uint32_t r;
-  asm("v_pk_min_u16 %0, %1, 1 op_sel_hi:[1,0]" : "=v"(r) : "v"(a));
+  asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
   return r;
 }
-__device__ __forceinline__ uint32_t pk_vsub1_u16(uint32_t a) {
+__device__ __forceinline__ uint32_t pk_vsubsat_i16(uint32_t a, uint32_t b) {
   uint32_t r;
-  asm("v_pk_sub_u16 %0, %1, 1 op_sel_hi:[1,0]" : "=v"(r) : "v"(a));
+  asm("v_pk_sub_i16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "s"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vmax_i16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_max_i16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
 __device__ __forceinline__ uint32_t pk_vasr15_i16(uint32_t a) {
@@ -200,22 +210,44 @@ __device__ __forceinline__ uint32_t pk_vbfi(uint32_t m, uint32_t a, uint32_t b) 
   return r;
 }
 #pragma clang diagnostic pop
-__device__ __forceinline__ uint32_t gelu_pair_common(uint32_t w, const uint16_t *__restrict__ tab) {
+// Nonzero when either code of the pair leaves gelu_pair_common's domain: a
+// NaN or an infinity (magnitude >= 0x7F80) or a nonzero magnitude below
+// 0x0100 (exponent field 0 or 1).  Per half, mag + c sets bit 15 exactly when
+// mag >= 0x8000 - c, and no sum carries into the next half (mag <= 0x7FFF).
+__device__ __forceinline__ uint32_t gelu_pair_special(uint32_t w) {
+  const uint32_t mag = w & 0x7FFF7FFFu;
+  const uint32_t nonzero = mag + 0x7FFF7FFFu;  // mag >= 1
+  const uint32_t normal = mag + 0x7F007F00u;   // mag >= 0x0100
+  const uint32_t inf_nan = mag + 0x00800080u;  // mag >= 0x7F80
+  return ((nonzero & ~normal) | inf_nan) & 0x80008000u;
+}
+
+// gelu_pair_common in two steps, so that a caller can issue the table reads of
+// many pairs before it needs any of them: the table index of both codes (and
+// the clamped offsets, which mark |x| < TLO), then the result from the two
+// table values.
+struct GeluPairIdx {
+  uint32_t off, idx;
+};
+__device__ __forceinline__ GeluPairIdx gelu_pair_index(uint32_t w) {
   constexpr uint32_t TLO2 = GELU_TLO | (GELU_TLO << 16);
-  constexpr uint32_t LIM2 = (GELU_PHI - GELU_TLO) | ((GELU_PHI - GELU_TLO) << 16);
-  constexpr uint32_t DLIM2 = (GELU_NHI - GELU_PHI) | ((GELU_NHI - GELU_PHI) << 16);
-  constexpr uint32_t NPOS2 = (uint32_t)GELU_NPOS | ((uint32_t)GELU_NPOS << 16);
+  constexpr uint32_t CLAMP2 = (uint32_t)GELU_SPAN | ((uint32_t)GELU_SPAN << 16);  // sentinel slot
+  constexpr uint32_t HALF2 = (uint32_t)GELU_HALF | ((uint32_t)GELU_HALF << 16);
   const uint32_t sgn = pk_vasr15_i16(w);                 // 0xFFFF per negative half
   const uint32_t off = pk_vsub_u16(w & 0x7FFF7FFFu, TLO2);
-  const uint32_t lim = pk_vadd_u16(sgn & DLIM2, LIM2);
-  const uint32_t idx0 = pk_vmin_u16(off, lim);
-  const uint32_t m_tab = pk_vsub1_u16(pk_vmin1_u16(off ^ idx0));  // 0xFFFF where off <= lim
-  const uint32_t idx = pk_vadd_u16v(idx0, sgn & NPOS2);
-  const uint32_t tv = (uint32_t)tab[idx & 0xFFFFu] | ((uint32_t)tab[idx >> 16] << 16);
-  const uint32_t half = pack_bf(0.5f * lo_bf(w), 0.5f * hi_bf(w));
+  return {off, pk_vadd_u16v(pk_vmin_u16s(off, CLAMP2), sgn & HALF2)};
+}
+__device__ __forceinline__ uint32_t gelu_pair_finish(uint32_t w, uint32_t off, uint32_t tv) {
+  const uint32_t r = pk_vmin_u16(tv, w);                 // table value, or x / -0 above it
+  // exponent field - 1 (signed saturation keeps -0; the max keeps +0)
+  const uint32_t half = pk_vmax_i16(pk_vsubsat_i16(w, 0x00800080u), w & 0x80008000u);
   const uint32_t m_small = pk_vasr15_i16(off);           // 0xFFFF where |x| < TLO
-  const uint32_t big = pk_vbfi(sgn, 0x80008000u, w);       // above the table: x, or -0
-  return pk_vbfi(m_tab, tv, pk_vbfi(m_small, half, big));
+  return pk_vbfi(m_small, half, r);
+}
+__device__ __forceinline__ uint32_t gelu_pair_common(uint32_t w, const uint16_t *__restrict__ tab) {
+  const GeluPairIdx t = gelu_pair_index(w);
+  const uint32_t tv = (uint32_t)tab[t.idx & 0xFFFFu] | ((uint32_t)tab[t.idx >> 16] << 16);
+  return gelu_pair_finish(w, t.off, tv);
 }
 
 // Both codes of a pair through the exact per-element rules.
