@@ -189,7 +189,7 @@ PK_API int pk_gemm_set_ring_depth(int depth);
  *     block_m x block_n output tile, block_k = k-tile per LDS stage,
  *     shared_memory_stages = LDS ring depth, vector_width = bf16 per global
  *     load (8, or 1 on the unaligned path), unroll = 32x32x16 MFMA k-steps
- *     per stage.  Variants: 256x256x32 DMA ring of 4 or 5 stages (4 waves),
+ *     per stage.  Variants: 256x256x32 DMA ring of 4 or 5 stages (8 waves),
  *     256x256x64 register-staged (8 waves), 128x128x64 and 64x64x64 (4 waves).
  *   int8 (matmul_int8, matmul_int8_gelu, matmul_int8_residual): block_n =
  *     output columns per workgroup, split over num_warps waves of 16..256

@@ -287,9 +287,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// Large-tile GEMM (the MLP block path).  256x256 per workgroup, 4 waves in a
-// 2x2 grid, each wave owning a 128x128 sub-tile (16 MFMA accumulator blocks,
-// 256 fp32 per lane, held in AGPRs).  K advances in tiles of 32 through a
+// Large-tile GEMM (the MLP block path).  256x256 per workgroup, W = 8 waves
+// in a 4x2 grid, each wave owning a 64x128 sub-tile (8 MFMA accumulator
+// blocks, 128 fp32 per lane), two waves per SIMD: while one waits at the
+// barrier, on its LDS reads or on issuing its DMA, the other keeps the matrix
+// core busy (W = 4, one wave per SIMD with 128x128 sub-tiles, is the other
+// instantiation: config-2 GEMM1 474 -> 452 us, GEMM2 443 -> 423 us going from
+// 4 to 8 waves, bit-identical).  K advances in tiles of 32 through a
 // STAGES-deep LDS ring (4 or 5) filled by buffer_load_dwordx4 ... lds
 // (global -> LDS without VGPR staging) issued STAGES-1 tiles ahead.  Per
 // k-tile and wave:
@@ -304,8 +308,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
 // (their results are never stored).
 // ---------------------------------------------------------------------------
 constexpr int G2_BM = 256, G2_BN = 256, G2_BK = 32, G2_STAGES = 4;
-constexpr int G2_THREADS = 256;
-constexpr int G2_DMA_PER_TILE = 8;  // 1 KiB global_load_lds per wave per tile: 4 for A, 4 for B
+constexpr int G2_WAVES = 8;
+constexpr int G2_THREADS = G2_WAVES * 64;
 
 // A rows of 64 B (the DMA kernel's 32-wide k-tiles): the 16 rows of a read
 // group fall 4 to each 64-byte quarter of the banks by row & 3, and
@@ -313,9 +317,19 @@ constexpr int G2_DMA_PER_TILE = 8;  // 1 KiB global_load_lds per wave per tile: 
 // & 3 left 2-way conflicts).
 __device__ __forceinline__ int swz_a32(int row) { return (row >> 2) & 3; }
 
-template <int EPI, int STAGES>
-__global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
+template <int EPI, int STAGES, int W = G2_WAVES>
+__global__ __launch_bounds__(W * 64, 1) void gemm_dma_kernel(GemmArgs g) {
   static_assert(STAGES == 4 || STAGES == 5, "ring depth");
+  static_assert(W == 4 || W == 8, "waves");
+  constexpr int NTHR = W * 64;
+  constexpr int WMN = W / 2;            // waves along M (two along N)
+  constexpr int TM = G2_BM / WMN;       // rows per wave: 128 or 64
+  constexpr int FM = TM / 32;           // 32-row MFMA blocks per wave
+  constexpr int NA = 16 / W, NB = 16 / W;  // 1 KiB DMA loads per wave per k-tile
+  constexpr int DPT = NA + NB;
+  constexpr int NU = FM + 4;            // fragment-read units per substep
+  constexpr int NM = FM * 4;            // MFMAs per substep
+  constexpr int NJ = 4096 / NTHR;       // 16-byte epilogue chunks per thread per half
   constexpr int A_STAGE = G2_BM * G2_BK;  // elements
   constexpr int B_STAGE = G2_BK * G2_BN;
   // One array per ring stage: distinct LDS objects let the compiler see that a
@@ -357,19 +371,19 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   // offset (voffset) and the per-tile advance as the scalar soffset, so the
   // issue needs no address arithmetic in vector registers.
   // A: wave w, instr j covers rows 64w + 16j + lane/4, physical chunk lane%4.
-  uint32_t a_off[4];
+  uint32_t a_off[NA];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 64 * wid + 16 * j + (lane >> 2);
+  for (int j = 0; j < NA; ++j) {
+    const int r = (G2_BM / W) * wid + 16 * j + (lane >> 2);
     const int c = (lane & 3) ^ swz_a32(r);
     const int rr = min(r, g.M - 1 - m0);
     a_off[j] = (uint32_t)(rr * g.K + 8 * c) * 2u;
   }
   // B: wave w, instr j covers rows 8w + 2j + lane/32, physical chunk lane%32.
-  uint32_t b_off[4];
+  uint32_t b_off[NB];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 8 * wid + 2 * j + (lane >> 5);
+  for (int j = 0; j < NB; ++j) {
+    const int r = (G2_BK / W) * wid + 2 * j + (lane >> 5);
     const int c = (lane & 31) ^ swz_b<G2_BN>(r);
     const int cc = min(8 * c, g.N - 8 - n0);
     b_off[j] = (uint32_t)(r * g.N + cc) * 2u;
@@ -377,21 +391,22 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   const pk_u32x4 a_rsrc = rsrc_words(g.A + (size_t)m0 * g.K, (uint32_t)((size_t)(g.M - m0) * g.K * 2));
   const pk_u32x4 b_rsrc = rsrc_words(g.B + n0, (uint32_t)(((size_t)g.K * g.N - n0) * 2));
   auto issue_one = [&](auto c, int t, int j) __attribute__((always_inline)) {
-    if (j < 4)
-      dma_lds16(a_rsrc, &a_stage(c)[(64 * wid + 16 * j) * G2_BK], a_off[j], t * (G2_BK * 2));
+    if (j < NA)
+      dma_lds16(a_rsrc, &a_stage(c)[((G2_BM / W) * wid + 16 * j) * G2_BK], a_off[j], t * (G2_BK * 2));
     else
-      dma_lds16(b_rsrc, &b_stage(c)[(8 * wid + 2 * (j - 4)) * G2_BN], b_off[j - 4], t * (G2_BK * 2) * g.N);
+      dma_lds16(b_rsrc, &b_stage(c)[((G2_BK / W) * wid + 2 * (j - NA)) * G2_BN], b_off[j - NA],
+                t * (G2_BK * 2) * g.N);
   };
   auto issue = [&](auto c, int t) {
 #pragma unroll
-    for (int j = 0; j < G2_DMA_PER_TILE; ++j) issue_one(c, t, j);
+    for (int j = 0; j < DPT; ++j) issue_one(c, t, j);
   };
 
   // ---- per-lane fragment read offsets (elements within a stage)
-  int a_rd[4][2];
+  int a_rd[FM][2];
 #pragma unroll
-  for (int fm = 0; fm < 4; ++fm) {
-    const int row = wm * 128 + fm * 32 + (lane & 31);
+  for (int fm = 0; fm < FM; ++fm) {
+    const int row = wm * TM + fm * 32 + (lane & 31);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int c = 2 * s + (lane >> 5);
@@ -413,7 +428,7 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
       }
 
   struct Frag {
-    bf16x8 a[4];
+    bf16x8 a[FM];
     bf16x8 b[4];
   };
   // Fragment reads in 8 units (u < 4: A block u; u >= 4: B block u-4, two
@@ -424,10 +439,10 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
     const uint16_t *as = a_stage(c);
     const uint16_t *bs = b_stage(c);
     const int fm = u;
-    if (u < 4) {
+    if (u < FM) {
       f.a[fm] = lds_read_a(as + a_rd[fm][s]);
     } else {
-      const int fn = u - 4;
+      const int fn = u - FM;
       const i16x4 h0 = lds_read_tr(bs + b_rd[fn][s][0]);
       const i16x4 h1 = lds_read_tr(bs + b_rd[fn][s][1]);
       f.b[fn] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -435,11 +450,11 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   };
   auto read_frag = [&](Frag &f, auto c, int s) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) read_unit(f, c, s, u);
+    for (int u = 0; u < NU; ++u) read_unit(f, c, s, u);
   };
-  f32x16 acc[4][4];
+  f32x16 acc[FM][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -466,8 +481,8 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   issue(S2{}, min(2, KT - 1));
   if constexpr (STAGES > 4) issue(S3{}, min(3, KT - 1));
 #pragma unroll
-  for (int j = 0; j < 4; ++j) issue_one(SL{}, min(STAGES - 1, KT - 1), j);
-  vm_wait<(STAGES - 2) * G2_DMA_PER_TILE + 4>();
+  for (int j = 0; j < NA; ++j) issue_one(SL{}, min(STAGES - 1, KT - 1), j);
+  vm_wait<(STAGES - 2) * DPT + NA>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");  // no LDS access moves above the barrier
   __builtin_amdgcn_sched_barrier(0);
@@ -492,25 +507,33 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
     using Prev = std::integral_constant<int, (st + STAGES - 1) % STAGES>;
     const int tp_dma = min(t + STAGES - 1, KT - 1);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < NM; ++i) {
       mfma_one(f0, i);
-      if ((i & 1) == 0) read_unit(f1, c, 1, i >> 1);
-      if ((i & 3) == 1) issue_one(Prev{}, tp_dma, 4 + (i >> 2));
+      if constexpr (W == 4) {
+        if ((i & 1) == 0) read_unit(f1, c, 1, i >> 1);
+      } else {
+        if (i < NU) read_unit(f1, c, 1, i);
+      }
+      if ((i & 3) == 1) issue_one(Prev{}, tp_dma, NA + (i >> 2));
       __builtin_amdgcn_sched_barrier(0);
     }
     // this wave's reads of stage st are done and its DMA of tile t+1 landed
     // (STAGES-2 newer tiles may still be in flight); then all waves agree.
     lgkm_wait0();
-    vm_wait<(STAGES - 2) * G2_DMA_PER_TILE>();
+    vm_wait<(STAGES - 2) * DPT>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS access moves above the barrier
     __builtin_amdgcn_sched_barrier(0);
     const int tn_dma = min(t + STAGES, KT - 1);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < NM; ++i) {
       mfma_one(f1, i);
       if ((i & 3) == 1) issue_one(c, tn_dma, i >> 2);
-      if ((i & 1) == 0) read_unit(f0, Next{}, 0, i >> 1);
+      if constexpr (W == 4) {
+        if ((i & 1) == 0) read_unit(f0, Next{}, 0, i >> 1);
+      } else {
+        if (i < NU) read_unit(f0, Next{}, 0, i);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -564,17 +587,17 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
   uint16_t *tab_lds = Bs2;
   if constexpr (EPI == EPI_BIAS_GELU) {
     static_assert(GELU_TABLE_SIZE <= B_STAGE, "GELU table fits in one ring array");
-    for (int i = tid; i < (GELU_TABLE_SIZE + 1) / 2; i += G2_THREADS)
+    for (int i = tid; i < (GELU_TABLE_SIZE + 1) / 2; i += NTHR)
       reinterpret_cast<uint32_t *>(tab_lds)[i] = reinterpret_cast<const uint32_t *>(g.gelu_tab)[i];
   }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    if (wm == h) {
+    if (wm / (WMN / 2) == h) {
 #pragma unroll
-      for (int fm = 0; fm < 4; ++fm)
+      for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          uint16_t *blk = ep_block(fm * 4 + q);
+          uint16_t *blk = ep_block((wm % (WMN / 2)) * (TM / 8) + fm * 4 + q);
 #pragma unroll
           for (int fn = 0; fn < 4; ++fn) {
             const int col = wn * 128 + fn * 32 + (lane & 31);
@@ -588,15 +611,15 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
     }
     __syncthreads();
     if constexpr (EPI == EPI_BIAS_GELU) {
-      // The whole half at once: all 16 chunks of a thread are read and biased
+      // The whole half at once: all NJ chunks of a thread are read and biased
       // first, one wave vote picks the paired GELU (no NaN or infinity in the
       // wave's half) or the exact per-element one for all of them, then every
       // table lookup is issued before any result is stored.
-      uint32_t u[16][4];
+      uint32_t u[NJ][4];
       uint32_t special = 0;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = (tid + j * G2_THREADS) >> 5;
+      for (int j = 0; j < NJ; ++j) {
+        const int r = (tid + j * NTHR) >> 5;
         const u32x4 tv = *reinterpret_cast<const u32x4 *>(ep_block(r >> 3) + (r & 7) * EP_LD + 8 * c_thr);
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -624,9 +647,9 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
         };
         fetch(0, 0);
 #pragma unroll
-        for (int j0 = 0; j0 < 16; j0 += G) {
+        for (int j0 = 0; j0 < NJ; j0 += G) {
           const int b = (j0 / G) & 1;
-          if (j0 + G < 16) fetch(b ^ 1, j0 + G);
+          if (j0 + G < NJ) fetch(b ^ 1, j0 + G);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int jj = 0; jj < G; ++jj)
@@ -636,13 +659,13 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
           for (int w = 0; w < 4; ++w) u[j][w] = gelu_pair_exact(u[j][w], tab_lds);
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = (tid + j * G2_THREADS) >> 5;
+      for (int j = 0; j < NJ; ++j) {
+        const int r = (tid + j * NTHR) >> 5;
         const int m = m0 + h * 128 + r, n = n0 + 8 * c_thr;
         if (m < g.M && n < g.N)
           *reinterpret_cast<u32x4 *>(Cp + (size_t)m * g.N + n) = u32x4{u[j][0], u[j][1], u[j][2], u[j][3]};
@@ -651,8 +674,8 @@ __global__ __launch_bounds__(G2_THREADS, 1) void gemm_dma_kernel(GemmArgs g) {
       continue;
     }
 #pragma unroll 4
-    for (int j = 0; j < 16; ++j) {
-      const int qd = tid + j * G2_THREADS;
+    for (int j = 0; j < NJ; ++j) {
+      const int qd = tid + j * NTHR;
       const int r = qd >> 5, c = qd & 31;  // c == c_thr
       const int m = m0 + h * 128 + r, n = n0 + 8 * c;
       if (m < g.M && n < g.N) {

@@ -93,7 +93,7 @@ def test_gemm_config_unavailable_is_an_error(gpu):
     assert ei.value.code == _lib.PK_ERR_UNSUPPORTED
     # the DMA ring needs K % 32 == 0: asking for it at K = 72 is refused, not run
     a2, b2 = to_dev(int_bf16((64, 72), 3)), to_dev(int_bf16((72, 64), 4))
-    dma = dict(block_m=256, block_n=256, block_k=32, num_warps=4, vector_width=8, unroll=2, shared_memory_stages=5)
+    dma = dict(block_m=256, block_n=256, block_k=32, num_warps=8, vector_width=8, unroll=2, shared_memory_stages=5)
     with pytest.raises(_lib.PolyKernelError):
         gemm_cfg(0, a2, b2, dma)
 
