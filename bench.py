@@ -439,8 +439,8 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": read_traffic(),
-                     "kernel": f"gemm_dma_kernel<EPI_BIAS_GELU,{entries[0]['best']['shared_memory_stages']}> "
-                               "(GEMM1: x@W1+b1->GELU, 2^39 FLOP/launch)"},
+                     "kernel": f"gemm_dma_kernel<EPI_BIAS_GELU,{entries[0]['best']['shared_memory_stages']},"
+                               f"{entries[0]['best']['num_warps']},4> (GEMM1: x@W1+b1->GELU, 2^39 FLOP/launch)"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -288,12 +288,14 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
 
 // ---------------------------------------------------------------------------
 // Large-tile GEMM (the MLP block path).  256x256 per workgroup, W = 8 waves
-// in a 4x2 grid, each wave owning a 64x128 sub-tile (8 MFMA accumulator
-// blocks, 128 fp32 per lane), two waves per SIMD: while one waits at the
-// barrier, on its LDS reads or on issuing its DMA, the other keeps the matrix
-// core busy (W = 4, one wave per SIMD with 128x128 sub-tiles, is the other
-// instantiation: config-2 GEMM1 474 -> 452 us, GEMM2 443 -> 423 us going from
-// 4 to 8 waves, bit-identical).  K advances in tiles of 32 through a
+// in a 2x4 grid (WNN = 4 along N), each wave owning a 128x64 sub-tile (8 MFMA
+// accumulator blocks, 128 fp32 per lane), two waves per SIMD: while one waits
+// at the barrier, on its LDS reads or on issuing its DMA, the other keeps the
+// matrix core busy.  Other instantiations of the template: W = 4 (one wave
+// per SIMD, 128x128 sub-tiles; config-2 GEMM1 474 -> 452 us and GEMM2
+// 443 -> 423 us going to 8 waves) and the 4x2 grid of 64x128 sub-tiles (0.5 %
+// slower than 2x4: two more LDS read instructions per substep); all
+// bit-identical.  K advances in tiles of 32 through a
 // STAGES-deep LDS ring (4 or 5) filled by buffer_load_dwordx4 ... lds
 // (global -> LDS without VGPR staging) issued STAGES-1 tiles ahead.  Per
 // k-tile and wave:
@@ -308,7 +310,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(GemmArgs g) {
 // (their results are never stored).
 // ---------------------------------------------------------------------------
 constexpr int G2_BM = 256, G2_BN = 256, G2_BK = 32, G2_STAGES = 4;
-constexpr int G2_WAVES = 8;
+constexpr int G2_WAVES = 8, G2_WAVES_N = 4;
 constexpr int G2_THREADS = G2_WAVES * 64;
 
 // A rows of 64 B (the DMA kernel's 32-wide k-tiles): the 16 rows of a read
@@ -317,18 +319,20 @@ constexpr int G2_THREADS = G2_WAVES * 64;
 // & 3 left 2-way conflicts).
 __device__ __forceinline__ int swz_a32(int row) { return (row >> 2) & 3; }
 
-template <int EPI, int STAGES, int W = G2_WAVES>
+template <int EPI, int STAGES, int W = G2_WAVES, int WNN = G2_WAVES_N>
 __global__ __launch_bounds__(W * 64, 1) void gemm_dma_kernel(GemmArgs g) {
   static_assert(STAGES == 4 || STAGES == 5, "ring depth");
   static_assert(W == 4 || W == 8, "waves");
   constexpr int NTHR = W * 64;
-  constexpr int WMN = W / 2;            // waves along M (two along N)
-  constexpr int TM = G2_BM / WMN;       // rows per wave: 128 or 64
+  constexpr int WMN = W / WNN;          // waves along M (WNN along N)
+  constexpr int TM = G2_BM / WMN;       // rows per wave
+  constexpr int TN = G2_BN / WNN;       // columns per wave
   constexpr int FM = TM / 32;           // 32-row MFMA blocks per wave
+  constexpr int FN = TN / 32;           // 32-column MFMA blocks per wave
   constexpr int NA = 16 / W, NB = 16 / W;  // 1 KiB DMA loads per wave per k-tile
   constexpr int DPT = NA + NB;
-  constexpr int NU = FM + 4;            // fragment-read units per substep
-  constexpr int NM = FM * 4;            // MFMAs per substep
+  constexpr int NU = FM + FN;           // fragment-read units per substep
+  constexpr int NM = FM * FN;           // MFMAs per substep
   constexpr int NJ = 4096 / NTHR;       // 16-byte epilogue chunks per thread per half
   constexpr int A_STAGE = G2_BM * G2_BK;  // elements
   constexpr int B_STAGE = G2_BK * G2_BN;
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_dma_kernel(GemmArgs g) {
   // wave index as a scalar: every LDS destination (M0) below is then computed
   // in scalar registers
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid / WNN, wn = wid % WNN;
   const int tm = (g.M + G2_BM - 1) / G2_BM, tn = (g.N + G2_BN - 1) / G2_BN;
   int mt, nt;
   tile_coords(blockIdx.x, tm, tn, mt, nt);
@@ -414,22 +418,22 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_dma_kernel(GemmArgs g) {
     }
   }
   const int grp = lane >> 4, gi = lane & 15;
-  int b_rd[4][2][2];
+  int b_rd[FN][2][2];
 #pragma unroll
-  for (int fn = 0; fn < 4; ++fn)
+  for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const int k = 16 * s + 8 * (grp >> 1) + 4 * r + (gi >> 2);
-        const int col = wn * 128 + fn * 32 + 16 * (grp & 1) + 4 * (gi & 3);
+        const int col = wn * TN + fn * 32 + 16 * (grp & 1) + 4 * (gi & 3);
         const int c = col >> 3;
         b_rd[fn][s][r] = k * G2_BN + ((c ^ swz_b<G2_BN>(k)) << 3) + (col & 7);
       }
 
   struct Frag {
     bf16x8 a[FM];
-    bf16x8 b[4];
+    bf16x8 b[FN];
   };
   // Fragment reads in 8 units (u < 4: A block u; u >= 4: B block u-4, two
   // transpose reads joined without repacking) so they can be spread over the
@@ -452,17 +456,17 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int u = 0; u < NU; ++u) read_unit(f, c, s, u);
   };
-  f32x16 acc[FM][4];
+  f32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   auto mfma_one = [&](const Frag &f, int i) {
-    acc[i >> 2][i & 3] =
-        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i >> 2], f.b[i & 3], acc[i >> 2][i & 3], 0, 0, 0);
+    acc[i / FN][i % FN] =
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i / FN], f.b[i % FN], acc[i / FN][i % FN], 0, 0, 0);
   };
 
   using S0 = std::integral_constant<int, 0>;
@@ -599,8 +603,8 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_dma_kernel(GemmArgs g) {
         for (int q = 0; q < 4; ++q) {
           uint16_t *blk = ep_block((wm % (WMN / 2)) * (TM / 8) + fm * 4 + q);
 #pragma unroll
-          for (int fn = 0; fn < 4; ++fn) {
-            const int col = wn * 128 + fn * 32 + (lane & 31);
+          for (int fn = 0; fn < FN; ++fn) {
+            const int col = wn * TN + fn * 32 + (lane & 31);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int r = (lane >> 5) * 4 + e;
