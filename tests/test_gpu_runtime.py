@@ -85,6 +85,31 @@ def test_every_gemm_config_epilogues_bit_exact(gpu, oracle, epi):
         assert np.array_equal(got, want), cfg
 
 
+def test_gemm_gelu_epilogue_zeros_tiny_and_special_codes(gpu, oracle):
+    """The 256x256 DMA kernel's GELU epilogue on exact codes: with B = 0 every
+    output is GELU(bias[n]), so the bias row chooses the epilogue's inputs.
+    Column tile 0 holds tiny magnitudes (exponent field 0 or 1), infinities and
+    NaNs, which send its waves to the per-element rules; column tile 1 holds
+    +-0, the smallest magnitudes the paired rules take, both table edges and
+    the sentinel range, which stay on the paired path."""
+    M, N, Kd = 256, 512, 64
+    a = int_bf16((M, Kd), 71)
+    b = np.zeros((Kd, N), dtype=np.uint16)
+    rng = np.random.default_rng(72)
+    bias = synth.normal_bf16((N,), 73, 2.0)
+    special = [0x0001, 0x007F, 0x0080, 0x00FF, 0x8001, 0x80FF, 0x7F80, 0xFF80, 0x7FC0, 0xFFC1]
+    bias[rng.choice(256, size=len(special), replace=False)] = special
+    common = [0x0000, 0x8000, 0x0100, 0x8100, 0x3B4A, 0xBB4A, 0x3B4B, 0xBB4B, 0x4031, 0x4032,
+              0x40B1, 0xC0B1, 0x40B2, 0xC0B2, 0x7F7F, 0xFF7F]
+    bias[256 + rng.choice(256, size=len(common), replace=False)] = common
+    want = oracle.fused_matmul_bias_gelu(a, b, bias)
+    dma = dict(block_m=256, block_n=256, block_k=32, num_warps=8, vector_width=8, unroll=2, shared_memory_stages=5)
+    got = from_dev(gemm_cfg(1, to_dev(a), to_dev(b), dma, bias=to_dev(bias)))
+    nan = ((want & 0x7F80) == 0x7F80) & ((want & 0x7F) != 0)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all(((got[nan] & 0x7F80) == 0x7F80) & ((got[nan] & 0x7F) != 0))
+
+
 def test_gemm_config_unavailable_is_an_error(gpu):
     a, b = to_dev(int_bf16((64, 64), 1)), to_dev(int_bf16((64, 64), 2))
     cfg = dict(block_m=96, block_n=96, block_k=32, num_warps=4, vector_width=8, unroll=2, shared_memory_stages=5)
