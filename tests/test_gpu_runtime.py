@@ -85,6 +85,22 @@ def test_every_gemm_config_epilogues_bit_exact(gpu, oracle, epi):
         assert np.array_equal(got, want), cfg
 
 
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_dma_partial_tiles_bit_exact(gpu, oracle, epi):
+    """The 256x256 DMA kernel on a grid whose last tile row and column are
+    partial (M = 300, N = 264): clamped loads, masked stores, every epilogue."""
+    M, N, Kd = 300, 264, 96
+    a, b = int_bf16((M, Kd), 74), int_bf16((Kd, N), 75)
+    bias = synth.normal_bf16((N,), 76, 0.5)
+    r = synth.normal_bf16((M, N), 77)
+    want = {0: lambda: oracle.matmul(a, b), 1: lambda: oracle.fused_matmul_bias_gelu(a, b, bias),
+            2: lambda: oracle.fused_matmul_bias_residual(a, b, bias, r)}[epi]()
+    dma = dict(block_m=256, block_n=256, block_k=32, num_warps=8, vector_width=8, unroll=2, shared_memory_stages=5)
+    got = from_dev(gemm_cfg(epi, to_dev(a), to_dev(b), dma, bias=to_dev(bias) if epi else None,
+                            r=to_dev(r) if epi == 2 else None))
+    assert np.array_equal(got, want)
+
+
 def test_gemm_gelu_epilogue_zeros_tiny_and_special_codes(gpu, oracle):
     """The 256x256 DMA kernel's GELU epilogue on exact codes: with B = 0 every
     output is GELU(bias[n]), so the bias row chooses the epilogue's inputs.
