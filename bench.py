@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: the config-2 fused MLP block on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 40]
 
 A step is one pass of the MLP block over the config-2 batch (BASELINE.json
 configs[1]): RMSNorm(x, gamma) -> MatMul W1 [4096,16384] + b1 -> GELU(erf) ->
