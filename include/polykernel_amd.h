@@ -176,10 +176,6 @@ PK_API int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C
                       const uint16_t *bias, const uint16_t *R, int M, int N, int K, int tile,
                       void *stream);
 
-/* Tuning hook: k-tiles in flight in the DMA-pipelined GEMM's LDS ring (4 or 5;
- * 5 uses all 160 KiB of LDS).  Process-wide; default 5. */
-PK_API int pk_gemm_set_ring_depth(int depth);
-
 /* ---- configurations (tuning-cache vocabulary) ------------------------------ */
 
 /* One kernel configuration; the fields are those of the tuning-cache schema
@@ -260,10 +256,15 @@ PK_API int pk_probe_invalid_launch(int *launch_status, int *sync_status);
 
 /* ---- code-object support ----------------------------------------------------- */
 /* What a host needs to launch the emitted code objects: the device GELU table
- * of the current device (built on first use) and the library-owned
- * per-device workspace (grown on demand, kept until the process ends). */
+ * of the current device (built on first use) and the library-owned workspace
+ * of (current device, stream): a buffer of at least `bytes` for launches on
+ * `stream` (hipStream_t; NULL = the null stream), grown on demand without a
+ * device synchronisation, kept until the process ends.  Each stream has its
+ * own buffer, so launches on different streams never share scratch; threads
+ * that feed ONE stream must serialise their launch sequences themselves (the
+ * library's own entry points hold the slot's lock while they enqueue). */
 PK_API int pk_gelu_table(const uint16_t **table);
-PK_API int pk_library_workspace(size_t bytes, void **ptr);
+PK_API int pk_library_workspace(size_t bytes, void *stream, void **ptr);
 
 /* ---- naive device goldens (the autotuner's correctness gate) --------------- */
 /* Straightforward one-thread-per-output kernels that restate the reference
@@ -290,6 +291,26 @@ PK_API int pk_naive_attention(const uint16_t *Q, const uint16_t *K, const uint16
  * Definitions of tests/golden/metrics.py:20-77.  Synchronous on `stream`;
  * allocates a small device buffer. */
 PK_API int pk_compare_bf16(const uint16_t *got, const uint16_t *want, long long n, double out[4], void *stream);
+
+/* Error-model gate of the autotuner for GEMM-class outputs: *bad (host) =
+ * number of outputs of `got` that are NOT the reference epilogue applied to
+ * some fp32 accumulation of the same products, i.e. outside the values the
+ * epilogue takes over accumulators t in S +- delta, S the exact (fp64) sum,
+ * delta = (K 2^-23 + operand_ulps 2^-8) sum|p| for bf16 operands (operand_ulps
+ * admits that many bf16 ulps of difference in each A element, as a fused
+ * RMSNorm prologue may round a normalised activation to the neighbouring
+ * bf16), (K + 2) 2^-23 sum|p| for int8 weights (the reference's per-element
+ * dequantisation rounds twice per product).  Any summation order passes; a
+ * wrong index, sign, dropped term or dropped bias does not.  epi as
+ * pk_naive_matmul / pk_naive_matmul_int8.  Synchronous on `stream`; allocates
+ * a small device buffer.  Not derived from the reference (which gates fused
+ * ops on cosine / pcc only, tools/polykernel-bench/bench.py:297-306). */
+PK_API int pk_gate_matmul(int epi, const uint16_t *A, const uint16_t *B, const uint16_t *bias, const uint16_t *R,
+                          const uint16_t *got, int M, int N, int K, double operand_ulps, unsigned long long *bad,
+                          void *stream);
+PK_API int pk_gate_matmul_int8(int epi, const uint16_t *A, const int8_t *Wq, const float *scale,
+                               const uint16_t *R, const uint16_t *got, int M, int N, int K,
+                               unsigned long long *bad, void *stream);
 
 /* ---- synthetic inputs (host, deterministic, OpenMP) -------------------- */
 

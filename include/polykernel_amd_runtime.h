@@ -160,10 +160,10 @@ PK_API int pk_emit_code_object(pk_kernel_cache *cache, const char *entry_json, c
 
 /* ---- autotuner ------------------------------------------------------------ */
 /* Sweep (op, shape) on the current device.  options_json may be NULL or an
- * object with any of: warmup, iters, rotate_bytes, rel_ceiling, max_variants,
- * seed, batch_heads, verbose.  Result -> pk_last_text():
- * {"entry": <schema entry>, "variants": [{"config", "name", "validated",
- * "time_ms", "correctness"}, ...]}. */
+ * object with any of: warmup, iters, rounds, rotate_bytes, rel_ceiling,
+ * max_variants, seed, batch_heads, verbose, inject_broken.  Result ->
+ * pk_last_text(): {"entry": <schema entry>, "variants": [{"config", "name",
+ * "validated", "time_ms", "model_violations", "correctness"}, ...]}. */
 PK_API int pk_autotune(const char *op, long long M, long long N, long long K, const char *dtype,
                        const char *options_json);
 

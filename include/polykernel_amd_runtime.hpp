@@ -149,6 +149,9 @@ struct VariantResult {
   Correctness correctness;
   bool validated = false;
   std::optional<double> time_ms;  // nullopt <=> failed the gate, never timed
+  // GEMM-class ops: outputs outside the fp32 error model (pk_gate_matmul*);
+  // a validated variant has none.  nullopt for ops gated on the metrics only.
+  std::optional<unsigned long long> model_violations;
   bool operator==(const VariantResult &) const = default;
 };
 // Fastest validated variant; ties go to the lowest index; nullopt if none.
@@ -228,6 +231,10 @@ struct AutotuneOptions {
   std::uint64_t seed = 0xC0FFEE;
   int batch_heads = 32;  // B*H for fused_kv_append_attention
   bool verbose = false;
+  // Test hook (tools/polykernel-bench/bench.py --inject-broken of the
+  // reference): add one fast-but-wrong variant, named "broken_fast ...", that
+  // the gate must reject -- GEMM-class ops only.
+  bool inject_broken = false;
 };
 
 struct AutotuneResult {
@@ -237,7 +244,8 @@ struct AutotuneResult {
 
 // Sweep the candidates of (op, shape) on the current device: every variant is
 // first compared with a naive device reference of the op on seeded inputs
-// (cosine / max_rel_err / pcc); only variants that pass the gate are timed
+// (cosine / max_rel_err / pcc; GEMM-class ops also the fp32 error model of
+// pk_gate_matmul*); only variants that pass the gate are timed
 // (HIP events, median of `iters`); the fastest validated one becomes the
 // entry.  Returns false with `error` when the sweep could not run.
 PK_API bool Autotune(std::string_view op, const Shape &shape, const AutotuneOptions &options,

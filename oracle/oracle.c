@@ -7,8 +7,15 @@
  *
  * Each function cites the reference file:line whose arithmetic it follows.
  * Pinning (how each function is checked, besides this restatement):
- *   - bf16 conversion: exhaustive 2^32 sweep against the closed form
- *     (tests/test_oracle.py::test_bf16_rne_exhaustive_closed_form).
+ *   - bf16 conversion: on the host, a structured sweep (all 65536 upper
+ *     halves x 10 rounding classes of the dropped bits) against torch's RNE
+ *     conversion and the NaN rule (tests/test_oracle.py::
+ *     test_bf16_rne_structured_sweep); the exhaustive 2^32 comparison runs on
+ *     the device against the hardware conversion (tests/test_gpu_parity.py).
+ *   - add / bias: a structured sweep (every exponent difference 0..26, both
+ *     signs, all mantissa pairs, subnormals, overflow, +-0, +-inf, NaN, random
+ *     pairs) against numpy fp32 addition + torch RNE
+ *     (tests/test_oracle.py::test_add_matches_independent_bf16_add).
  *   - rmsnorm / gelu / matmul / softmax / fused_*: bit-exact against the
  *     reference's own kernels/cpu drivers compiled into oracle/_ref, plus the
  *     hand-computed known answers of tests/golden/test_golden_self.py.
@@ -17,7 +24,7 @@
  *     closed-form cases (S_kv=1 -> O=V, K=0 -> O=mean(V), exact int sums).
  *   - quantize: closed-form properties (max|wq|=127, zero column, exact ties
  *     round half-even) -- the reference has no C++ quantizer.
- *   - residual_rmsnorm / softmax_mask / bias / add / mlp_block / decode chain:
+ *   - residual_rmsnorm / softmax_mask / mlp_block / decode chain:
  *     compositions of the pinned primitives, checked against the _ref drivers
  *     chained stage by stage.
  */

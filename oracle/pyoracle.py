@@ -97,6 +97,15 @@ def add(a, b):
     return out
 
 
+def bias(x, b):
+    """golden.bias (tests/golden/golden.py:53-55): bf16(f32(x[i, j]) + f32(b[j]))."""
+    x, b = _u16(x), _u16(b)
+    out = np.empty_like(x)
+    N = x.shape[-1]
+    lib().pko_bias(_p(x), _p(b), _p(out), x.size // N, N)
+    return out
+
+
 def residual_rmsnorm(x, r, w=None, eps=1e-5):
     x, r = _u16(x), _u16(r)
     out = np.empty_like(x)

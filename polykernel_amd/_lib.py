@@ -83,7 +83,6 @@ SIGNATURES = {
     "pk_decode_mlp_int8_workspace_size": (SZ, [I, I, I]),
     "launch_decode_mlp_int8": (I, [P, P, P, P, P, P, I, I, I, P, SZ, P]),
     "pk_gemm_ex": (I, [I, P, P, P, P, P, I, I, I, I, P]),
-    "pk_gemm_set_ring_depth": (I, [I]),
     "pk_int8_default_config": (I, [I, I, I, C.POINTER(Config)]),
     "pk_matmul_int8_ex": (I, [I, P, P, P, P, P, I, I, I, C.POINTER(Config), P, SZ, P]),
     "pk_gemm_config_ex": (I, [I, P, P, P, P, P, I, I, I, C.POINTER(Config), P]),
@@ -94,6 +93,8 @@ SIGNATURES = {
     "pk_naive_rmsnorm": (I, [P, P, P, P, I, I, F, P]),
     "pk_naive_softmax_mask": (I, [P, P, P, I, I, P]),
     "pk_naive_attention": (I, [P, P, P, P, I, I, I, I, I, F, I, P]),
+    "pk_gate_matmul": (I, [I, P, P, P, P, P, I, I, I, D, C.POINTER(C.c_ulonglong), P]),
+    "pk_gate_matmul_int8": (I, [I, P, P, P, P, P, I, I, I, C.POINTER(C.c_ulonglong), P]),
     "pk_compare_bf16": (I, [P, P, LL, C.POINTER(D), P]),
     # runtime layer (include/polykernel_amd_runtime.h)
     "pk_last_text": (C.c_char_p, []),
@@ -121,7 +122,7 @@ SIGNATURES = {
     "pk_emit_code_object": (I, [P, C.c_char_p, C.c_char_p, C.c_char_p]),
     "pk_gelu_table": (I, [C.POINTER(P)]),
     "pk_probe_invalid_launch": (I, [C.POINTER(I), C.POINTER(I)]),
-    "pk_library_workspace": (I, [SZ, C.POINTER(P)]),
+    "pk_library_workspace": (I, [SZ, P, C.POINTER(P)]),
     "pk_runtime_destroy": (None, [P]),
     "pk_runtime_resolve": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p]),
     "pk_runtime_run": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p, P]),

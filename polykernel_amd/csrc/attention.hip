@@ -822,15 +822,15 @@ int attention_dp(AttArgs g, hipStream_t st) {
   g.q_tiles = (g.S_q + AT_BQ - 1) / AT_BQ;
   const int kv_tiles = (g.S_kv + AT_BKV - 1) / AT_BKV;
   g.splits = pick_splits(g.BH, g.q_tiles, kv_tiles);
+  WorkspaceLease lease;  // held until the combine kernel is queued
   if (g.splits > 1) {
     const size_t rows = (size_t)g.BH * g.S_q;
     const size_t bytes_o = (size_t)g.splits * rows * DP * sizeof(float);
     const size_t bytes = bytes_o + (size_t)g.splits * rows * 2 * sizeof(float);
-    void *ws = nullptr;
-    int rc = library_workspace(bytes, &ws);
+    int rc = library_workspace(bytes, st, lease);
     if (rc) return rc;
-    g.part_o = static_cast<float *>(ws);
-    g.part_ml = reinterpret_cast<float *>(static_cast<char *>(ws) + bytes_o);
+    g.part_o = static_cast<float *>(lease.ptr);
+    g.part_ml = reinterpret_cast<float *>(static_cast<char *>(lease.ptr) + bytes_o);
   }
   const int blocks = g.BH * g.q_tiles * g.splits;
   if (aligned) attention_kernel<DP, true><<<blocks, AT_THREADS, 0, st>>>(g);
@@ -889,15 +889,15 @@ int attention_fa(FaArgs a, int D, int qg, hipStream_t st) {
   const int ntiles = (a.S_kv + BKV - 1) / BKV;
   a.splits = 1;
   while ((int64_t)a.BH * a.q_tiles * a.splits < 256 && ntiles / (2 * a.splits) >= 8 && a.splits < 8) a.splits *= 2;
+  WorkspaceLease lease;  // held until the merge kernel is queued
   if (a.splits > 1) {
     const size_t rows = (size_t)a.BH * a.S_q;
     const size_t bytes_o = (size_t)a.splits * rows * D * sizeof(float);
     const size_t bytes = bytes_o + (size_t)a.splits * rows * 2 * sizeof(float);
-    void *ws = nullptr;
-    int rc = library_workspace(bytes, &ws);
+    int rc = library_workspace(bytes, st, lease);
     if (rc) return rc;
-    a.part_o = static_cast<float *>(ws);
-    a.part_ml = reinterpret_cast<float *>(static_cast<char *>(ws) + bytes_o);
+    a.part_o = static_cast<float *>(lease.ptr);
+    a.part_ml = reinterpret_cast<float *>(static_cast<char *>(lease.ptr) + bytes_o);
   }
   const int blocks = a.BH * a.q_tiles * a.splits;
   const bool fused = a.Kn != nullptr;

@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -19,8 +20,17 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 bool g_table_ready[kMaxDevices] = {};
 const uint16_t *g_table_ptr[kMaxDevices] = {};
-void *g_ws_ptr[kMaxDevices] = {};
-size_t g_ws_bytes[kMaxDevices] = {};
+
+// One workspace slot per (device, stream); slots live until the process ends
+// (their addresses stay valid for leases), buffers a slot outgrew stay
+// allocated beside it (`retired`).
+struct WsSlot {
+  std::mutex mu;
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  std::vector<void *> retired;
+};
+std::map<std::pair<int, uintptr_t>, WsSlot *> g_ws_slots;  // guarded by g_mu
 }  // namespace
 
 void set_error(const char *fmt, ...) {
@@ -114,27 +124,32 @@ int gelu_table(const uint16_t **table) {
   return PK_OK;
 }
 
-int library_workspace(size_t bytes, void **ptr) {
+int library_workspace(size_t bytes, void *st, WorkspaceLease &lease) {
   int dev = 0;
   PK_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= kMaxDevices) {
     set_error("device ordinal %d out of range", dev);
     return PK_ERR_UNSUPPORTED;
   }
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (g_ws_bytes[dev] < bytes) {
-    if (g_ws_ptr[dev]) {
-      // Earlier launches may still read the old buffer.
-      PK_HIP(hipDeviceSynchronize());
-      PK_HIP(hipFree(g_ws_ptr[dev]));
-      g_ws_ptr[dev] = nullptr;
-      g_ws_bytes[dev] = 0;
-    }
-    size_t want = std::max<size_t>(bytes, size_t(1) << 20);
-    PK_HIP(hipMalloc(&g_ws_ptr[dev], want));
-    g_ws_bytes[dev] = want;
+  WsSlot *slot;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    WsSlot *&s = g_ws_slots[{dev, reinterpret_cast<uintptr_t>(st)}];
+    if (!s) s = new WsSlot;
+    slot = s;
   }
-  *ptr = g_ws_ptr[dev];
+  std::unique_lock<std::mutex> lk(slot->mu);
+  if (slot->bytes < bytes) {
+    size_t want = size_t(1) << 20;
+    while (want < bytes) want <<= 1;
+    void *p = nullptr;
+    PK_HIP(hipMalloc(&p, want));
+    if (slot->ptr) slot->retired.push_back(slot->ptr);
+    slot->ptr = p;
+    slot->bytes = want;
+  }
+  lease.ptr = slot->ptr;
+  lease.lock = std::move(lk);
   return PK_OK;
 }
 
@@ -235,12 +250,15 @@ int pk_gelu_table(const uint16_t **table) {
   return gelu_table(table);
 }
 
-int pk_library_workspace(size_t bytes, void **ptr) {
+int pk_library_workspace(size_t bytes, void *stream, void **ptr) {
   if (!ptr) {
     set_error("pk_library_workspace: null argument");
     return PK_ERR_INVALID_ARG;
   }
-  return library_workspace(bytes, ptr);
+  WorkspaceLease lease;
+  int rc = library_workspace(bytes, stream, lease);
+  if (rc == PK_OK) *ptr = lease.ptr;
+  return rc;
 }
 
 int pk_init(void) {

@@ -392,7 +392,10 @@ __global__ __launch_bounds__(W * 64, 1) void gemm_dma_kernel(GemmArgs g) {
     const int cc = min(8 * c, g.N - 8 - n0);
     b_off[j] = (uint32_t)(r * g.N + cc) * 2u;
   }
-  const pk_u32x4 a_rsrc = rsrc_words(g.A + (size_t)m0 * g.K, (uint32_t)((size_t)(g.M - m0) * g.K * 2));
+  // Every A offset stays inside this tile's (at most) 256 rows, so the
+  // record count is that panel's size, which fits 32 bits whenever 256 * K * 2
+  // does (checked by the dispatcher) -- the whole remaining matrix need not.
+  const pk_u32x4 a_rsrc = rsrc_words(g.A + (size_t)m0 * g.K, (uint32_t)((size_t)min(g.M - m0, G2_BM) * g.K * 2));
   const pk_u32x4 b_rsrc = rsrc_words(g.B + n0, (uint32_t)(((size_t)g.K * g.N - n0) * 2));
   auto issue_one = [&](auto c, int t, int j) __attribute__((always_inline)) {
     if (j < NA)
@@ -730,9 +733,6 @@ int launch_tile(const GemmArgs &g, bool aligned, hipStream_t st) {
   return PK_OK;
 }
 
-// Ring depth of gemm_dma_kernel (tuning knob, see pk_gemm_set_ring_depth).
-int g_ring_depth = 5;
-
 template <int EPI>
 int gemm_dispatch(const GemmArgs &g, int tile, hipStream_t st) {
   const bool aligned = (g.K % 8 == 0) && (g.N % 8 == 0) && aligned16(g.A) && aligned16(g.B);
@@ -741,8 +741,7 @@ int gemm_dispatch(const GemmArgs &g, int tile, hipStream_t st) {
   const bool ep_aligned = aligned16(g.C) && (!g.R || aligned16(g.R)) && (!g.bias || aligned16(g.bias));
   if (tile == 0 && aligned && ep_aligned && offsets32 && g.K % G2_BK == 0 && g.N >= 8) {
     const int tiles = ((g.M + G2_BM - 1) / G2_BM) * ((g.N + G2_BN - 1) / G2_BN);
-    if (g_ring_depth == 5) gemm_dma_kernel<EPI, 5><<<tiles, G2_THREADS, 0, st>>>(g);
-    else gemm_dma_kernel<EPI, 4><<<tiles, G2_THREADS, 0, st>>>(g);
+    gemm_dma_kernel<EPI, 5><<<tiles, G2_THREADS, 0, st>>>(g);
     PK_LAUNCH_CHECK("gemm_dma_kernel");
     return PK_OK;
   }
@@ -832,7 +831,7 @@ bool gemm_default(int M, int N, int K, pk_config *out) {
   const int vw = (K % 8 == 0 && N % 8 == 0) ? 8 : 1;
   const int tile = pick_tile(M, N);
   int v = tile == 0 ? GV_REG256 : tile == 1 ? GV_REG128 : GV_REG64;
-  if (tile == 0 && vw == 8 && gemm_dma_shape_ok(N, K)) v = g_ring_depth == 5 ? GV_DMA5 : GV_DMA4;
+  if (tile == 0 && vw == 8 && gemm_dma_shape_ok(N, K)) v = GV_DMA5;
   *out = gemm_variant_config(v, vw);
   return true;
 }
@@ -1216,10 +1215,10 @@ int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_
     return PK_OK;
   }
   // Long rows: normalise once into library workspace, then the plain GEMM.
-  void *ws = nullptr;
-  int rc = library_workspace((size_t)M * K * 2, &ws);
+  WorkspaceLease lease;  // held until the GEMM that reads the panel is queued
+  int rc = library_workspace((size_t)M * K * 2, st, lease);
   if (rc) return rc;
-  uint16_t *a = static_cast<uint16_t *>(ws);
+  uint16_t *a = static_cast<uint16_t *>(lease.ptr);
   rc = rmsnorm_launch(x, gamma, a, M, K, eps, st);
   if (rc) return rc;
   return gemm_run(EPI_NONE, a, W, out, nullptr, nullptr, M, N, K, st);
@@ -1271,6 +1270,7 @@ int launch_fused_rmsnorm_matmul_gamma(const uint16_t *x, const uint16_t *gamma, 
 }
 
 size_t pk_mlp_block_workspace_size(int M, int d, int F) {
+  if (M <= 0 || d <= 0 || F <= 0) return 0;  // no launch takes a workspace
   auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
   return up((size_t)M * d * 2) + up((size_t)M * F * 2);
 }
@@ -1295,13 +1295,6 @@ int launch_mlp_block(const uint16_t *x, const uint16_t *gamma, const uint16_t *W
   rc = gemm_run(EPI_BIAS_GELU, a, W1, h, b1, nullptr, M, F, d, st);
   if (rc) return rc;
   return gemm_run(EPI_BIAS_RESID, h, W2, out, b2, x, M, d, F, st);
-}
-
-// Tuning hook: LDS ring depth (4 or 5 k-tiles) of the DMA-pipelined GEMM.
-int pk_gemm_set_ring_depth(int depth) {
-  PK_CHECK_ARG(depth == 4 || depth == 5, "pk_gemm_set_ring_depth: depth must be 4 or 5");
-  g_ring_depth = depth;
-  return PK_OK;
 }
 
 // Test/tuning hook: run one GEMM epilogue variant with an explicit tile choice

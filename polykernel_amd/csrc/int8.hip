@@ -280,7 +280,7 @@ struct I8sPlan {
 };
 
 bool i8s_shape_ok(int M, int N, int K) {
-  return N % 16 == 0 && K % I8S_KSTEP == 0 && (size_t)K * N < (size_t(1) << 31) &&
+  return M > 0 && N > 0 && K > 0 && N % 16 == 0 && K % I8S_KSTEP == 0 && (size_t)K * N < (size_t(1) << 31) &&
          (size_t)M * K * 2 < (size_t(1) << 31);
 }
 
@@ -399,6 +399,7 @@ bool int8_default(int M, int N, int K, pk_config *out) {
 // Workspace for the built-in choice, whichever kernel the pointers' alignment
 // leads to.
 size_t int8_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
   size_t need = 0;
   I8sPlan p;
   if (i8s_plan(M, N, K, nullptr, device_cus(), p)) need = i8s_workspace(p, M, N);
@@ -406,9 +407,13 @@ size_t int8_workspace_bytes(int M, int N, int K) {
   return std::max(need, s > 1 ? (size_t)s * M * N * sizeof(float) : 0);
 }
 
-static int use_workspace(size_t need, void *&ws, size_t ws_bytes) {
+static int use_workspace(size_t need, void *&ws, size_t ws_bytes, hipStream_t st, WorkspaceLease &lease) {
   if (need == 0) return PK_OK;
-  if (ws == nullptr) return library_workspace(need, &ws);
+  if (ws == nullptr) {
+    int rc = library_workspace(need, st, lease);
+    ws = lease.ptr;
+    return rc;
+  }
   if (ws_bytes < need) {
     set_error("int8 matmul: workspace of %zu bytes required, got %zu", need, ws_bytes);
     return PK_ERR_WORKSPACE;
@@ -436,8 +441,9 @@ int int8_run(int epi, const uint16_t *A, const int8_t *W, const float *scale, ui
     return PK_ERR_UNSUPPORTED;
   }
   Int8Args g{A, W, scale, nullptr, C, R, tab, M, N, K, 1, 0};
+  WorkspaceLease lease;  // library scratch, held until the reduction is queued
   if (fast) {
-    int rc = use_workspace(i8s_workspace(plan, M, N), ws, ws_bytes);
+    int rc = use_workspace(i8s_workspace(plan, M, N), ws, ws_bytes, st, lease);
     if (rc) return rc;
     if (plan.splits > 1 && !aligned16(ws)) {
       set_error("int8 matmul: workspace must be 16-byte aligned");
@@ -454,7 +460,7 @@ int int8_run(int epi, const uint16_t *A, const int8_t *W, const float *scale, ui
     const int unit = I8_STEP * I8_WAVES;
     g.kper = ((K + g.splits - 1) / g.splits + unit - 1) / unit * unit;
     g.splits = (K + g.kper - 1) / g.kper;
-    int rc = use_workspace(g.splits > 1 ? (size_t)g.splits * M * N * sizeof(float) : 0, ws, ws_bytes);
+    int rc = use_workspace(g.splits > 1 ? (size_t)g.splits * M * N * sizeof(float) : 0, ws, ws_bytes, st, lease);
     if (rc) return rc;
     g.partial = static_cast<float *>(ws);
     const bool aligned = (N % 16 == 0) && (K % 8 == 0) && aligned16(A) && aligned16(W);
@@ -524,6 +530,7 @@ int pk_matmul_int8_ex(int epi, const uint16_t *A, const int8_t *Wq, const float 
 }
 
 size_t pk_decode_mlp_int8_workspace_size(int M, int d, int F) {
+  if (M <= 0 || d <= 0 || F <= 0) return 0;  // no launch takes a workspace
   auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
   const size_t p = std::max(int8_workspace_bytes(M, F, d), int8_workspace_bytes(M, d, F));
   return up((size_t)M * F * 2) + up(p);

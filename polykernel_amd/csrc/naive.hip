@@ -234,6 +234,139 @@ __global__ __launch_bounds__(kThreads) void metrics_pass2(const uint16_t *__rest
 
 int grid1d(int64_t n, int per_block = kThreads) { return (int)((n + per_block - 1) / per_block); }
 
+// ---- the autotuner's error-model gate ---------------------------------------
+// An output of a GEMM-class op passes when it is what the reference's epilogue
+// gives for SOME fp32 accumulation of the same products.  Any order of an fp32
+// sum of K terms lies within K 2^-24 sum|p| of the exact sum (the classic
+// gamma_K bound), two such sums within twice that, so the accumulator t may be
+// anywhere in S +- delta, delta = (K 2^-23 + extra) sum|p|, with S and sum|p|
+// exact (fp64; bf16 x bf16 and bf16 x int8 x fp32 products are exact there).
+// RNE is monotone, so bf16(t) lies between the codes of the interval's ends;
+// bias and residual adds are non-decreasing in t, GELU decreases below its
+// minimum at x ~ -0.7518 and increases above, so the epilogue maps that code
+// range onto [lo, hi] computed from the ends -- by a scan of every code when
+// the range is short, else from the ends plus GELU's minimum where the range
+// straddles it.  A wrong index, sign, dropped term or dropped bias moves most
+// outputs outside; summation order alone never does.
+struct GateArgs {
+  int mode;  // 0: bf16 x bf16, 1: bf16 x int8 (per-column scale)
+  int epi;   // bf16: 0 none, 1 bias + GELU, 2 bias (optional) + residual, 3 residual;
+             // int8: 0 none, 1 GELU, 2 residual
+  const uint16_t *A;
+  const uint16_t *B;
+  const int8_t *Wq;
+  const float *scale;
+  const uint16_t *bias;
+  const uint16_t *R;
+  const uint16_t *got;
+  const uint16_t *tab;
+  int M, N, K;
+  double rel;  // K 2^-23 (+ extra) per unit of sum|p|
+  unsigned long long *bad;
+};
+
+__device__ __forceinline__ int bf_key(uint32_t b) { return (b & 0x8000u) ? -(int)(b & 0x7FFFu) : (int)b; }
+__device__ __forceinline__ uint32_t bf_from_key(int k) { return k >= 0 ? (uint32_t)k : (0x8000u | (uint32_t)(-k)); }
+
+// Lower (upper) bound on bf16(t) over every fp32 t >= x (t <= x): the code of
+// the largest fp32 value <= x (smallest >= x).
+__device__ __forceinline__ uint32_t bf_bound(double x, bool upper) {
+  float f = (float)x;
+  if (upper && (double)f < x) f = nextafterf(f, INFINITY);
+  if (!upper && (double)f > x) f = nextafterf(f, -INFINITY);
+  return f2bf(f);
+}
+
+__device__ __forceinline__ float gate_gelu(uint32_t u, const uint16_t *tab) { return bf2f(gelu_bits(u, tab)); }
+
+__global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs g) {
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  bool bad = false;
+  if (idx < (int64_t)g.M * g.N) {
+    const int m = (int)(idx / g.N), n = (int)(idx % g.N);
+    const uint16_t *a = g.A + (size_t)m * g.K;
+    double S = 0.0, T = 0.0;
+    if (g.mode == 0) {
+      for (int k = 0; k < g.K; ++k) {
+        const double p = (double)bf2f(a[k]) * (double)bf2f(g.B[(size_t)k * g.N + n]);
+        S += p;
+        T += fabs(p);
+      }
+    } else {
+      const double sc = (double)g.scale[n];
+      for (int k = 0; k < g.K; ++k) {
+        const double p = (double)bf2f(a[k]) * ((double)g.Wq[(size_t)k * g.N + n] * sc);
+        S += p;
+        T += fabs(p);
+      }
+    }
+    const double delta = g.rel * T * (1.0 + 0x1p-20) + g.K * 0x1p-149;
+    uint32_t clo = bf_bound(S - delta, false), chi = bf_bound(S + delta, true);
+    const float r = g.R ? bf2f(g.R[idx]) : 0.0f;
+    const bool gelu = g.epi == 1;
+    float lo, hi;
+    if (gelu) {
+      uint32_t ulo = clo, uhi = chi;
+      if (g.mode == 0) {  // u = bf16(bf16(t) + bias)
+        const float b = bf2f(g.bias[n]);
+        ulo = f2bf(bf2f(clo) + b);
+        uhi = f2bf(bf2f(chi) + b);
+      }
+      const int kl = bf_key(ulo), kh = bf_key(uhi);
+      lo = INFINITY;
+      hi = -INFINITY;
+      if (kh - kl <= 512) {
+        for (int kk = kl; kk <= kh; ++kk) {
+          const float v = gate_gelu(bf_from_key(kk), g.tab);
+          lo = fminf(lo, v);
+          hi = fmaxf(hi, v);
+        }
+      } else {
+        const float vl = gate_gelu(ulo, g.tab), vh = gate_gelu(uhi, g.tab);
+        lo = fminf(vl, vh);
+        hi = fmaxf(vl, vh);
+        if (bf2f(ulo) < -0.5f && bf2f(uhi) > -1.0f)  // the minimum lies in [-1, -0.5]
+          for (uint32_t c = 0xBF00u; c <= 0xBF80u; ++c) lo = fminf(lo, gate_gelu(c, g.tab));
+      }
+    } else {
+      auto f = [&](uint32_t c) -> float {
+        float v = bf2f(c);
+        if (g.mode == 0 && g.epi == 2 && g.bias) v = bf2f(f2bf(v + bf2f(g.bias[n])));
+        if (g.R) v = bf2f(f2bf(v + r));
+        return v;
+      };
+      lo = f(clo);
+      hi = f(chi);
+    }
+    const float got = bf2f(g.got[idx]);
+    bad = !(got >= lo && got <= hi);
+  }
+  const unsigned long long votes = __ballot(bad);
+  if ((threadIdx.x & 63) == 0 && votes) atomicAdd(g.bad, (unsigned long long)__popcll(votes));
+}
+
+int run_gate(GateArgs g, unsigned long long *bad_host, hipStream_t st) {
+  *bad_host = 0;
+  if ((int64_t)g.M * g.N == 0) return PK_OK;
+  if (g.epi == 1) {
+    int rc = gelu_table(&g.tab);
+    if (rc) return rc;
+  }
+  unsigned long long *d = nullptr;
+  PK_HIP(hipMalloc(&d, sizeof *d));
+  hipError_t e = hipMemsetAsync(d, 0, sizeof *d, st);
+  g.bad = d;
+  if (e == hipSuccess) {
+    gate_kernel<<<grid1d((int64_t)g.M * g.N), kThreads, 0, st>>>(g);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(bad_host, d, sizeof *d, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  (void)hipFree(d);
+  return e == hipSuccess ? PK_OK : hip_fail(e, "error-model gate");
+}
+
+
 }  // namespace
 }  // namespace pk
 
@@ -297,6 +430,29 @@ int pk_naive_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V, 
                                                                                         kv_stride, D, scale, causal);
   PK_LAUNCH_CHECK("naive_attention_kernel");
   return PK_OK;
+}
+
+int pk_gate_matmul(int epi, const uint16_t *A, const uint16_t *B, const uint16_t *bias, const uint16_t *R,
+                   const uint16_t *got, int M, int N, int K, double operand_ulps, unsigned long long *bad,
+                   void *stream) {
+  PK_CHECK_ARG(A && B && got && bad, "pk_gate_matmul: null argument");
+  PK_CHECK_ARG(epi >= 0 && epi <= 3, "pk_gate_matmul: epilogue %d not in 0..3", epi);
+  PK_CHECK_ARG((epi != 1 || bias) && (epi < 2 || R), "pk_gate_matmul: epilogue operand missing");
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && operand_ulps >= 0, "pk_gate_matmul: invalid argument");
+  GateArgs g{0, epi, A, B, nullptr, nullptr, epi == 1 || epi == 2 ? bias : nullptr, epi >= 2 ? R : nullptr, got,
+             nullptr, M, N, K, K * 0x1p-23 + operand_ulps * 0x1p-8, nullptr};
+  return run_gate(g, bad, (hipStream_t)stream);
+}
+
+int pk_gate_matmul_int8(int epi, const uint16_t *A, const int8_t *Wq, const float *scale, const uint16_t *R,
+                        const uint16_t *got, int M, int N, int K, unsigned long long *bad, void *stream) {
+  PK_CHECK_ARG(A && Wq && scale && got && bad && (epi != 2 || R), "pk_gate_matmul_int8: null argument");
+  PK_CHECK_ARG(epi >= 0 && epi <= 2, "pk_gate_matmul_int8: epilogue %d not in 0..2", epi);
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "pk_gate_matmul_int8: invalid shape");
+  // the reference rounds w*scale and a*(w*scale) once each before the sum
+  GateArgs g{1, epi, A, nullptr, Wq, scale, nullptr, epi == 2 ? R : nullptr, got, nullptr, M, N, K,
+             (K + 2) * 0x1p-23, nullptr};
+  return run_gate(g, bad, (hipStream_t)stream);
 }
 
 int pk_compare_bf16(const uint16_t *got, const uint16_t *want, long long n, double out[4], void *stream) {

@@ -13,6 +13,7 @@
 #include <string>
 
 #include "../../include/polykernel_amd.h"
+#include "workspace.hpp"
 
 namespace pk {
 
@@ -52,8 +53,6 @@ inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3
 // use.  Returns its device address for the current device (kernels take it as
 // an argument).
 int gelu_table(const uint16_t **table);
-// Library-owned per-device scratch for entry points without a workspace arg.
-int library_workspace(size_t bytes, void **ptr);
 
 // Configurations in the tuning-cache vocabulary (each defined beside the
 // dispatcher it describes).  *_configs write min(total, cap) entries and

@@ -30,6 +30,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <functional>
 
 #include "../../../include/polykernel_amd_runtime.hpp"
@@ -89,6 +90,12 @@ std::vector<uint16_t> NormalBf16(size_t n, uint64_t seed, uint64_t stream, doubl
 struct Workload {
   std::function<int(const pk_config *, int, hipStream_t)> run;
   std::function<int(hipStream_t)> golden;
+  // GEMM-class ops: outputs of out[0] outside the fp32 error model
+  // (pk_gate_matmul*), written to *bad
+  std::function<int(hipStream_t, unsigned long long *)> model;
+  // with AutotuneOptions::inject_broken: a fast-but-wrong variant (the
+  // default config on subtly wrong operands) the gate must reject
+  std::function<int(int, hipStream_t)> broken;
   std::vector<uint16_t *> out;
   size_t out_elems = 0;
   const uint16_t *want = nullptr;
@@ -119,6 +126,27 @@ bool AllocCopies(DeviceArena &arena, std::vector<T *> &bufs, int copies, size_t 
   return true;
 }
 
+// A copy of a [rows, cols] bf16 matrix with every 7th column scaled by 1.02:
+// outputs that use those columns move by ~2 %, while cosine and PCC over the
+// whole output stay above the reference gate's 0.999 / 0.99.
+uint16_t *PerturbedColumns(DeviceArena &arena, const std::vector<uint16_t> &host, size_t rows, size_t cols,
+                           std::string &error) {
+  std::vector<uint16_t> h = host;
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t c = 0; c < cols; c += 7) {
+      uint32_t u = (uint32_t)h[r * cols + c] << 16;
+      float f;
+      std::memcpy(&f, &u, 4);
+      f *= 1.02f;
+      std::memcpy(&u, &f, 4);
+      u += 0x7FFFu + ((u >> 16) & 1u);
+      h[r * cols + c] = (uint16_t)(u >> 16);
+    }
+  uint16_t *d = arena.Alloc<uint16_t>(h.size(), error);
+  if (!d || !Upload(d, h, error)) return nullptr;
+  return d;
+}
+
 bool PrepareGemm(std::string_view op, const Shape &s, const AutotuneOptions &o, DeviceArena &arena, Workload &w,
                  std::string &error) {
   const int epi = op == "matmul" ? 0 : op == "fused_matmul_bias_gelu" ? 1 : 2;
@@ -130,8 +158,8 @@ bool PrepareGemm(std::string_view op, const Shape &s, const AutotuneOptions &o, 
       !AllocCopies(arena, bias, w.copies, N, error) || !AllocCopies(arena, w.out, w.copies, c_n, error))
     return false;
   if (epi == 2 && !AllocCopies(arena, R, w.copies, c_n, error)) return false;
-  if (!Upload(A[0], NormalBf16(a_n, o.seed, 1, 1.0), error) ||
-      !Upload(B[0], NormalBf16(b_n, o.seed, 3, 1.0 / std::sqrt((double)K)), error) ||
+  const std::vector<uint16_t> b_host = NormalBf16(b_n, o.seed, 3, 1.0 / std::sqrt((double)K));
+  if (!Upload(A[0], NormalBf16(a_n, o.seed, 1, 1.0), error) || !Upload(B[0], b_host, error) ||
       !Upload(bias[0], NormalBf16(N, o.seed, 4, 0.02), error))
     return false;
   if (epi == 2 && !Upload(R[0], NormalBf16(c_n, o.seed, 5, 1.0), error)) return false;
@@ -150,6 +178,25 @@ bool PrepareGemm(std::string_view op, const Shape &s, const AutotuneOptions &o, 
     return pk_gemm_config_ex(epi, A[c], B[c], w.out[c], epi == 0 ? nullptr : bias[c], epi == 2 ? R[c] : nullptr, M,
                              N, K, cfg, st);
   };
+  w.model = [=](hipStream_t st, unsigned long long *bad) {
+    return pk_gate_matmul(epi, A[0], B[0], b1, epi == 2 ? R[0] : nullptr, w.out[0], M, N, K, 0.0, bad, st);
+  };
+  if (o.inject_broken) {
+    // with a bias: the bias dropped (a zero bias); plain matmul: perturbed columns
+    const uint16_t *Bb = B[0], *zb = nullptr;
+    if (epi == 0) {
+      if (!(Bb = PerturbedColumns(arena, b_host, K, N, error))) return false;
+    } else {
+      uint16_t *z = arena.Alloc<uint16_t>(N, error);
+      if (!z || !HipOk(hipMemset(z, 0, (size_t)N * 2), "hipMemset", error)) return false;
+      zb = z;
+    }
+    std::vector<uint16_t *> out = w.out;
+    w.broken = [=](int c, hipStream_t st) {
+      return pk_gemm_config_ex(epi, A[c], Bb, out[c], epi == 0 ? nullptr : zb, epi == 2 ? R[c] : nullptr, M, N, K,
+                               nullptr, st);
+    };
+  }
   return true;
 }
 
@@ -189,6 +236,23 @@ bool PrepareInt8(std::string_view op, const Shape &s, const AutotuneOptions &o, 
     return pk_matmul_int8_ex(epi, A[c], Wq[c], scale[c], w.out[c], epi == 2 ? R[c] : nullptr, M, N, K, cfg, nullptr,
                              0, st);
   };
+  w.model = [=](hipStream_t st, unsigned long long *bad) {
+    return pk_gate_matmul_int8(epi, A[0], Wq[0], scale[0], epi == 2 ? R[0] : nullptr, w.out[0], M, N, K, bad, st);
+  };
+  if (o.inject_broken) {
+    // every 7th column's scale off by 2 %
+    std::vector<float> hs(N);
+    if (!HipOk(hipMemcpy(hs.data(), scale[0], (size_t)N * 4, hipMemcpyDeviceToHost), "hipMemcpy D2H", error))
+      return false;
+    for (int j = 0; j < N; j += 7) hs[j] *= 1.02f;
+    float *bs = arena.Alloc<float>(N, error);
+    if (!bs || !Upload(bs, hs, error)) return false;
+    std::vector<uint16_t *> out = w.out;
+    w.broken = [=](int c, hipStream_t st) {
+      return pk_matmul_int8_ex(epi, A[c], Wq[c], bs, out[c], epi == 2 ? R[c] : nullptr, M, N, K, nullptr, nullptr,
+                               0, st);
+    };
+  }
   return true;
 }
 
@@ -201,9 +265,9 @@ bool PrepareRmsnormMatmul(const Shape &s, const AutotuneOptions &o, DeviceArena 
   if (!AllocCopies(arena, X, w.copies, x_n, error) || !AllocCopies(arena, W, w.copies, w_n, error) ||
       !AllocCopies(arena, G, w.copies, K, error) || !AllocCopies(arena, w.out, w.copies, c_n, error))
     return false;
+  const std::vector<uint16_t> w_host = NormalBf16(w_n, o.seed, 13, 1.0 / std::sqrt((double)K));
   if (!Upload(X[0], NormalBf16(x_n, o.seed, 11, 1.0), error) ||
-      !Upload(G[0], NormalBf16(K, o.seed, 12, 0.1, 1.0), error) ||
-      !Upload(W[0], NormalBf16(w_n, o.seed, 13, 1.0 / std::sqrt((double)K)), error))
+      !Upload(G[0], NormalBf16(K, o.seed, 12, 0.1, 1.0), error) || !Upload(W[0], w_host, error))
     return false;
   if (!Replicate(X, x_n, error) || !Replicate(W, w_n, error) || !Replicate(G, K, error)) return false;
   uint16_t *want = arena.Alloc<uint16_t>(c_n, error), *normed = arena.Alloc<uint16_t>(x_n, error);
@@ -218,6 +282,19 @@ bool PrepareRmsnormMatmul(const Shape &s, const AutotuneOptions &o, DeviceArena 
   w.run = [=](const pk_config *, int c, hipStream_t st) {
     return launch_fused_rmsnorm_matmul_gamma(X[c], G[c], W[c], w.out[c], M, N, K, 1e-6f, st);
   };
+  // the normalised activations of the golden are the GEMM's A operand; the
+  // fused prologue may round one to the neighbouring bf16 (1 ulp)
+  w.model = [=](hipStream_t st, unsigned long long *bad) {
+    return pk_gate_matmul(0, normed, W[0], nullptr, nullptr, w.out[0], M, N, K, 1.0, bad, st);
+  };
+  if (o.inject_broken) {
+    const uint16_t *Wb = PerturbedColumns(arena, w_host, K, N, error);
+    if (!Wb) return false;
+    std::vector<uint16_t *> out = w.out;
+    w.broken = [=](int c, hipStream_t st) {
+      return launch_fused_rmsnorm_matmul_gamma(X[c], G[c], Wb, out[c], M, N, K, 1e-6f, st);
+    };
+  }
   return true;
 }
 
@@ -377,6 +454,16 @@ bool Autotune(std::string_view op, const Shape &shape, const AutotuneOptions &o,
   DeviceArena arena;
   Workload w;
   if (!Prepare(op, shape, o, arena, w, error)) return false;
+  // the injected wrong variant runs as one more candidate (the default config
+  // on wrong operands), named so that it can be told apart
+  std::optional<size_t> broken;
+  if (o.inject_broken && w.broken) {
+    broken = cands.size();
+    cands.push_back(cands.front());
+  }
+  auto launch = [&](size_t i, const pk_config *pc, int copy, hipStream_t s) {
+    return broken && i == *broken ? w.broken(copy, s) : w.run(pc, copy, s);
+  };
   hipStream_t st = nullptr;
   if (!HipOk(hipStreamCreate(&st), "hipStreamCreate", error)) return false;
   struct StreamGuard {
@@ -386,16 +473,22 @@ bool Autotune(std::string_view op, const Shape &shape, const AutotuneOptions &o,
   if (!PkOk(w.golden(st), "golden", error) || !HipOk(hipStreamSynchronize(st), "golden", error)) return false;
 
   std::vector<VariantResult> results;
-  for (const Config &c : cands) {
+  for (size_t ci = 0; ci < cands.size(); ++ci) {
+    const Config &c = cands[ci];
     VariantResult v;
-    v.name = ToString(c);
+    v.name = broken && ci == *broken ? std::string("broken_fast ") + ToString(c) : ToString(c);
     const pk_config pc = ToPk(c);
     // poison: an element the variant does not write reads as NaN and fails
     bool ok = HipOk(hipMemsetAsync(w.out[0], 0xFF, w.out_elems * 2, st), "hipMemsetAsync", error);
-    int rc = ok ? w.run(&pc, 0, st) : PK_ERR_HIP;
+    int rc = ok ? launch(ci, &pc, 0, st) : PK_ERR_HIP;
     ok = ok && rc == PK_OK && HipOk(hipStreamSynchronize(st), "variant", error);
     double m[4] = {0, 0, 0, 0};
     if (ok) ok = pk_compare_bf16(w.out[0], w.want, w.compare_n, m, st) == PK_OK;
+    unsigned long long bad = 0;
+    if (ok && w.model) {
+      ok = w.model(st, &bad) == PK_OK;
+      if (ok) v.model_violations = bad;
+    }
     if (!ok) {
       if (o.verbose) std::fprintf(stderr, "[autotune] %s: launch failed: %s\n", v.name.c_str(), pk_last_error());
       (void)hipGetLastError();
@@ -405,10 +498,13 @@ bool Autotune(std::string_view op, const Shape &shape, const AutotuneOptions &o,
       continue;
     }
     v.correctness = Correctness{m[0], m[1], m[2]};
-    v.validated = PassesCorrectnessGate(v.correctness, ceiling);
+    // the reference's gate, and for GEMM-class ops every output inside the
+    // fp32 error model as well
+    v.validated = PassesCorrectnessGate(v.correctness, ceiling) && bad == 0;
     if (o.verbose)
-      std::fprintf(stderr, "[autotune] %s %s cosine=%.6f max_rel=%.3e pcc=%.6f %s\n", std::string(op).c_str(),
-                   v.name.c_str(), m[0], m[1], m[2], v.validated ? "PASS" : "REJECTED");
+      std::fprintf(stderr, "[autotune] %s %s cosine=%.6f max_rel=%.3e pcc=%.6f outside_model=%llu %s\n",
+                   std::string(op).c_str(), v.name.c_str(), m[0], m[1], m[2], bad,
+                   v.validated ? "PASS" : "REJECTED (correctness gate FAILED, NOT timed)");
     results.push_back(v);
   }
 
@@ -424,17 +520,17 @@ bool Autotune(std::string_view op, const Shape &shape, const AutotuneOptions &o,
   std::vector<std::vector<float>> samples(results.size());
   for (size_t i : timed) {  // initial warm-up of every variant
     const pk_config pc = ToPk(cands[i]);
-    for (int k = 0; k < o.warmup; ++k) (void)w.run(&pc, k % w.copies, st);
+    for (int k = 0; k < o.warmup; ++k) (void)launch(i, &pc, k % w.copies, st);
   }
   for (int r = 0; r < rounds; ++r) {
     for (size_t i : timed) {
       if (!results[i].validated) continue;
       const pk_config pc = ToPk(cands[i]);
-      (void)w.run(&pc, 0, st);
+      (void)launch(i, &pc, 0, st);
       for (int k = 0; k < per_round; ++k) {
         HipEventTimer t;
         t.Start(st);
-        const int rc = w.run(&pc, (r * per_round + k) % w.copies, st);
+        const int rc = launch(i, &pc, (r * per_round + k) % w.copies, st);
         t.Stop(st);
         const float ms = t.ElapsedMs();
         if (rc != PK_OK || ms < 0) {

@@ -246,6 +246,7 @@ PK_API int pk_autotune(const char *op, long long M, long long N, long long K, co
       else if (k == "seed" && i) o.seed = (uint64_t)*i;
       else if (k == "batch_heads" && i && *i > 0) o.batch_heads = (int)*i;
       else if (k == "verbose" && v.as_bool()) o.verbose = *v.as_bool();
+      else if (k == "inject_broken" && v.as_bool()) o.inject_broken = *v.as_bool();
       else return Fail(PK_ERR_INVALID_ARG, "pk_autotune: bad option '" + k + "'");
     }
   }
@@ -259,6 +260,9 @@ PK_API int pk_autotune(const char *op, long long M, long long N, long long K, co
                                     {"name", v.name},
                                     {"validated", v.validated},
                                     {"time_ms", v.time_ms ? pk::json::Value(*v.time_ms) : pk::json::Value()},
+                                    {"model_violations", v.model_violations
+                                                             ? pk::json::Value((long long)*v.model_violations)
+                                                             : pk::json::Value()},
                                     {"correctness", pk::autotune::detail::CorrectnessJson(c)}});
   }
   return Text(pk::json::Serialize(pk::json::Object{{"entry", pk::autotune::detail::EntryJson(res.entry)},

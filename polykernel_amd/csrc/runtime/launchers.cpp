@@ -16,6 +16,7 @@
 
 #include "../../../include/polykernel_amd_runtime.hpp"
 #include "../int8_args.h"
+#include "../workspace.hpp"
 
 namespace pk::runtime {
 
@@ -125,7 +126,13 @@ bool ModuleLaunch(void *fn, unsigned gx, unsigned gy, unsigned threads, void *st
 LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
   return [epi, table](const CacheEntry &e, void *io, std::string &error) {
     MatmulInt8IO *p = Cast<MatmulInt8IO>(io, error);
-    if (!p || !CheckEntry(e, p->M, p->N, p->K, error)) return false;
+    if (!p) return false;
+    // the linked path's argument check (pk_matmul_int8_ex), before any device call
+    if (!p->A || !p->Wq || !p->scale || !p->C || (epi == 2 && !p->residual)) {
+      error = "matmul_int8 code object: null tensor pointer";
+      return false;
+    }
+    if (!CheckEntry(e, p->M, p->N, p->K, error)) return false;
     const std::optional<CachedBinary> bin = table->cache.GetBinary(e.gpu, e.op, e.shape);
     if (!bin) {
       error = "no code object cached for " + FormatKey(e.gpu, e.op, e.shape) +
@@ -135,7 +142,7 @@ LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
     ModuleTable::Loaded *mod = table->Get(*bin, error);
     if (!mod) return false;
     if (!Aligned16(p->A) || !Aligned16(p->Wq) || !Aligned16(p->scale) || !Aligned16(p->C) ||
-        (epi == 2 && (!p->residual || !Aligned16(p->residual)))) {
+        (epi == 2 && !Aligned16(p->residual))) {
       error = "code-object int8 launch needs 16-byte aligned A, Wq, scale, C and residual";
       return false;
     }
@@ -146,6 +153,7 @@ LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
     const int slices = (p->N + c.block_n - 1) / c.block_n;
     const int mblocks = (p->M + c.block_m - 1) / c.block_m;
     void *ws = nullptr;
+    WorkspaceLease lease;  // library scratch, held until the reduction is queued
     if (splits > 1) {
       const size_t need = (size_t)splits * p->M * p->N * sizeof(float);
       if (p->workspace) {
@@ -154,9 +162,11 @@ LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
           return false;
         }
         ws = p->workspace;
-      } else if (pk_library_workspace(need, &ws) != PK_OK) {
+      } else if (library_workspace(need, p->stream, lease) != PK_OK) {
         error = std::string("library workspace: ") + pk_last_error();
         return false;
+      } else {
+        ws = lease.ptr;
       }
     }
     const uint16_t *tab = nullptr;

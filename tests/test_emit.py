@@ -73,7 +73,8 @@ def test_code_object_runtime_errors_before_any_device_call(tmp_path):
     e = int8_entry()
     cache.put(e)
     r = rt.Runtime(cache, fixed_arch="gfx950", code_objects=True)
-    io = rt.MatmulInt8IO(M=16, N=1024, K=2048)
+    # non-null placeholders: null operands are refused first (the linked path's check)
+    io = rt.MatmulInt8IO(A=16, Wq=16, scale=16, C=16, M=16, N=1024, K=2048)
     with pytest.raises(rt.RuntimeError_) as ei:
         r.run("matmul_int8_gelu", 16, 1024, 2048, io)
     assert "no code object cached" in ei.value.message

@@ -279,6 +279,100 @@ def test_autotune_small_shapes(gpu, op, M, N, Kd):
     assert e["time_ms"] == fastest
     # the library's default configuration is swept first
     assert res["variants"][0]["config"] == rt.default_config(op, M, N, Kd)
+    # GEMM-class ops are also gated on the fp32 error model: every validated
+    # variant has no output outside it
+    gemm_class = op.startswith(("matmul", "fused_matmul", "fused_rmsnorm_matmul"))
+    for v in res["variants"]:
+        assert (v["model_violations"] is not None) == gemm_class, v
+        if v["validated"] and gemm_class:
+            assert v["model_violations"] == 0, v
+
+
+BROKEN = [
+    ("fused_matmul_bias_gelu", 256, 256, 128),   # the reference's test_bench_gate.py:71-97 shape
+    ("fused_matmul_bias_residual", 256, 256, 1024),
+    ("matmul", 256, 512, 256),
+    ("matmul_int8_gelu", 16, 1024, 2048),
+    ("matmul_int8_residual", 32, 512, 1024),
+    ("fused_rmsnorm_matmul", 64, 512, 768),
+]
+
+
+@pytest.mark.parametrize("op,M,N,Kd", BROKEN)
+def test_autotune_rejects_broken_variant(gpu, op, M, N, Kd):
+    """A fast-but-wrong variant (the default config with the bias dropped, or
+    every 7th weight column / scale off by 2 %) passes the reference's metric
+    gate -- cosine >= 0.999, pcc >= 0.99, no max_rel ceiling for fused or
+    long-K ops -- but not the error model: it is rejected, never timed, never
+    best, and a real variant wins (tests/autotune/test_bench_gate.py:71-97)."""
+    _say(f"autotune {op} {M},{N},{Kd} with a broken variant")
+    res = rt.autotune(op, M, N, Kd, iters=3, warmup=1, max_variants=4, rotate_bytes=0, inject_broken=True)
+    broken = [v for v in res["variants"] if v["name"].startswith("broken_fast")]
+    assert len(broken) == 1, [v["name"] for v in res["variants"]]
+    b = broken[0]
+    assert not b["validated"] and b["time_ms"] is None, b
+    assert b["model_violations"] > 0, b
+    # the metrics alone would have let it through
+    assert b["correctness"]["cosine"] >= 0.999 and b["correctness"]["pcc"] >= 0.99, b
+    e = res["entry"]
+    assert e["validated"] and e["time_ms"] > 0
+    real = [v for v in res["variants"] if v["validated"]]
+    assert real and all(not v["name"].startswith("broken_fast") for v in real)
+    assert e["time_ms"] == min(v["time_ms"] for v in real)
+
+
+def test_gate_model_accepts_any_order_and_rejects_wrong_arithmetic(gpu, oracle):
+    """pk_gate_matmul on outputs made by the oracle (sequential order), by the
+    MFMA kernels (another order) and by three plausible mistakes."""
+    import ctypes
+
+    from polykernel_amd import _lib, kernels
+
+    lib = _lib.load()
+    M, N, Kd = 128, 192, 1024
+    a = synth.normal_bf16((M, Kd), 1)
+    b = synth.normal_bf16((Kd, N), 2, 1.0 / np.sqrt(Kd))
+    bias = synth.normal_bf16((N,), 3, 0.02)
+    r = synth.normal_bf16((M, N), 4)
+    da, db, dbias, dr = to_dev(a), to_dev(b), to_dev(bias), to_dev(r)
+
+    def bad_of(epi, got, bias_p=dbias, r_p=dr):
+        n = ctypes.c_ulonglong(0)
+        dg = to_dev(got)
+        _lib.check(lib.pk_gate_matmul(epi, _ptr(da), _ptr(db), _ptr(bias_p) if epi in (1, 2) else None,
+                                      _ptr(r_p) if epi >= 2 else None, _ptr(dg), M, N, Kd, 0.0,
+                                      ctypes.byref(n), _stream()), "gate")
+        return n.value
+
+    want = {0: oracle.matmul(a, b), 1: oracle.fused_matmul_bias_gelu(a, b, bias),
+            2: oracle.fused_matmul_bias_residual(a, b, bias, r)}
+    gpu_out = {0: from_dev(kernels.matmul(da, db)), 1: from_dev(kernels.fused_matmul_bias_gelu(da, db, dbias)),
+               2: from_dev(kernels.fused_matmul_bias_residual(da, db, dbias, dr))}
+    for epi in (0, 1, 2):
+        assert bad_of(epi, want[epi]) == 0, f"oracle output outside the model (epi {epi})"
+        assert bad_of(epi, gpu_out[epi]) == 0, f"kernel output outside the model (epi {epi})"
+    # mistakes: the last k term dropped, the bias dropped, B's columns shifted by one
+    dropped = oracle.matmul(a[:, :-1].copy(), b[:-1].copy())
+    assert bad_of(0, dropped) > M * N // 20
+    assert bad_of(1, oracle.fused_matmul_bias_gelu(a, b, np.zeros_like(bias))) > M * N // 5
+    shifted = oracle.matmul(a, np.roll(b, 1, axis=1))
+    assert bad_of(0, shifted) > M * N // 2
+
+    # int8: the reference's per-element dequantisation and the kernel both pass;
+    # one column's scale off by 2 % does not
+    wq, s = oracle.quantize_per_channel(b)
+    dwq, ds = to_dev(wq), to_dev(s)
+    n = ctypes.c_ulonglong(0)
+    for got in (oracle.matmul_int8(a, wq, s), from_dev(kernels.matmul_int8(da, dwq, ds))):
+        _lib.check(lib.pk_gate_matmul_int8(0, _ptr(da), _ptr(dwq), _ptr(ds), None, _ptr(to_dev(got)), M, N, Kd,
+                                           ctypes.byref(n), _stream()), "gate int8")
+        assert n.value == 0
+    s2 = s.copy()
+    s2[::7] *= np.float32(1.02)
+    wrong = oracle.matmul_int8(a, wq, s2)
+    _lib.check(lib.pk_gate_matmul_int8(0, _ptr(da), _ptr(dwq), _ptr(ds), None, _ptr(to_dev(wrong)), M, N, Kd,
+                                       ctypes.byref(n), _stream()), "gate int8")
+    assert n.value > (M * N // 7) // 2
 
 
 def test_autotune_gate_runs_before_timing(gpu):

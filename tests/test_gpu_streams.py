@@ -1,0 +1,141 @@
+"""Re-entrancy of the launchers and large-operand addressing (GPU).
+
+* Entry points whose reference signature has no workspace argument keep their
+  split partials in library scratch owned per (device, stream): launches of
+  split-K int8 and split-KV attention issued concurrently from two host
+  threads on two streams, and two threads sharing one stream, give the bits
+  of serial runs.
+* The DMA GEMM addresses A through a buffer descriptor whose 32-bit record
+  count covers only the tile's own 256 rows, so A operands of 4 GiB and more
+  are read in full (integer inputs: bit-exact against the oracle on rows
+  around the 2^32-byte boundary).
+"""
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+import pytest
+
+from tests.helpers import from_dev, int_bf16, rng_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _int8_case(seed, M=16, N=4096, Kd=8192):
+    rng = np.random.default_rng(seed)
+    a = rng_bf16((M, Kd), seed)
+    wq = rng.integers(-127, 128, size=(Kd, N)).astype(np.int8)
+    s = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+    return to_dev(a), to_dev(wq), to_dev(s)
+
+
+def _att_case(seed, B=1, H=2, Sq=64, Skv=4096, D=128):
+    return tuple(to_dev(rng_bf16(shape, seed + i))
+                 for i, shape in enumerate([(B, H, Sq, D), (B, H, Skv, D), (B, H, Skv, D)]))
+
+
+def _run_thread(fn, iters, results, idx, errors, stream):
+    import torch
+
+    try:
+        with torch.cuda.stream(stream):
+            outs = [fn(i) for i in range(iters)]
+        stream.synchronize()
+        results[idx] = [from_dev(o) for o in outs]
+    except Exception as e:  # noqa: BLE001 -- re-raised in the main thread
+        errors.append(e)
+
+
+def test_split_workspaces_concurrent_streams(gpu):
+    import torch
+
+    from polykernel_amd import kernels, runtime as rt
+
+    cfg = rt.default_config("matmul_int8", 16, 4096, 8192)
+    assert cfg["block_k"] < 8192, f"expected a split-K plan, got {cfg}"
+    i8 = [_int8_case(10 + j) for j in range(3)]
+    att = [_att_case(20 + 3 * j) for j in range(3)]
+    scale = 1.0 / np.sqrt(128)
+    run_i8 = lambda i: kernels.matmul_int8(*i8[i % 3])
+    run_att = lambda i: kernels.attention_prefill(*att[i % 3], scale=scale, causal=True)
+    _say("serial reference runs")
+    want_i8 = [from_dev(kernels.matmul_int8(*c)) for c in i8]
+    want_att = [from_dev(kernels.attention_prefill(*c, scale=scale, causal=True)) for c in att]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    results, errors = [None, None], []
+    iters = 24
+    t1 = threading.Thread(target=_run_thread, args=(run_i8, iters, results, 0, errors, s1))
+    t2 = threading.Thread(target=_run_thread, args=(run_att, iters, results, 1, errors, s2))
+    _say("concurrent: int8 split-K on stream 1, attention split-KV on stream 2")
+    t1.start(), t2.start()
+    t1.join(120), t2.join(120)
+    assert not errors, errors
+    assert not t1.is_alive() and not t2.is_alive()
+    for i in range(iters):
+        assert np.array_equal(results[0][i], want_i8[i % 3]), f"int8 launch {i} differs from the serial run"
+        assert np.array_equal(results[1][i], want_att[i % 3]), f"attention launch {i} differs from the serial run"
+
+
+def test_split_workspace_one_stream_two_threads(gpu):
+    """Two threads feeding ONE stream: each split-K launch's partial-sum and
+    reduction kernels stay adjacent in the stream (the workspace slot's lock
+    is held while they are enqueued)."""
+    import torch
+
+    from polykernel_amd import kernels
+
+    cases = [_int8_case(40 + j) for j in range(4)]
+    want = [from_dev(kernels.matmul_int8(*c)) for c in cases]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    results, errors = [None, None], []
+    iters = 32
+    t1 = threading.Thread(target=_run_thread,
+                          args=(lambda i: kernels.matmul_int8(*cases[i % 2]), iters, results, 0, errors, s))
+    t2 = threading.Thread(target=_run_thread,
+                          args=(lambda i: kernels.matmul_int8(*cases[2 + i % 2]), iters, results, 1, errors, s))
+    t1.start(), t2.start()
+    t1.join(120), t2.join(120)
+    assert not errors, errors
+    for i in range(iters):
+        assert np.array_equal(results[0][i], want[i % 2])
+        assert np.array_equal(results[1][i], want[2 + i % 2])
+
+
+def test_dma_gemm_a_operand_beyond_4gib(gpu, oracle):
+    """M = 262656, K = 8192: A is 4.3 GB (> 2^32 bytes).  Tile row 512 starts
+    where (M - m0) K 2 is exactly 2^32, the row block a whole-matrix record
+    count would have truncated to zero length."""
+    import torch
+
+    M, Kd, N = 262656, 8192, 256
+    assert M * Kd * 2 > 2**32
+    _say(f"matmul {M}x{N}x{Kd} (A {M * Kd * 2 / 2**30:.2f} GiB), integer inputs")
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    A = torch.empty((M, Kd), dtype=torch.bfloat16, device="cuda")
+    for r0 in range(0, M, 8192):
+        r1 = min(M, r0 + 8192)
+        A[r0:r1] = torch.randint(-3, 4, (r1 - r0, Kd), device="cuda", generator=gen).to(torch.bfloat16)
+    b = int_bf16((Kd, N), 8)
+    from polykernel_amd import kernels
+
+    C = kernels.matmul(A, to_dev(b))
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.arange(0, 4), np.arange(508, 516), np.arange(764, 772),
+                           np.arange(M - 262144 - 4, M - 262144 + 4), np.arange(M - 8, M),
+                           np.random.default_rng(9).choice(M, 16, replace=False)])
+    rows = np.unique(rows)
+    idx = torch.from_numpy(rows).cuda()
+    a_rows = from_dev(A.index_select(0, idx).contiguous())
+    got = from_dev(C.index_select(0, idx).contiguous())
+    want = oracle.matmul(a_rows, b)
+    bad = np.flatnonzero((got != want).any(axis=1))
+    assert bad.size == 0, f"rows {rows[bad][:10]} differ"
+    del A, C
+    torch.cuda.empty_cache()

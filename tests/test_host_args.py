@@ -1,0 +1,82 @@
+"""Host-side argument handling of the C-ABI, without a GPU.
+
+Every configuration and workspace-size query must answer degenerate shapes
+(zero or negative dims) with an error code or 0 -- never abort the process
+(the library's error convention: a status and pk_last_error, no abort).
+The queries run in a child process so a crash (SIGFPE, SIGSEGV) is reported
+as a failure instead of ending the test run.
+"""
+from __future__ import annotations
+
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+
+OPS = ["matmul", "fused_matmul_bias_gelu", "fused_matmul_bias_residual", "matmul_int8",
+       "matmul_int8_gelu", "matmul_int8_residual", "fused_rmsnorm_matmul", "fused_residual_rmsnorm",
+       "fused_softmax_mask", "fused_kv_append_attention"]
+
+_CHILD = r"""
+import ctypes as C, itertools, sys
+sys.path.insert(0, sys.argv[1])
+from polykernel_amd import _lib
+lib = C.CDLL(str(_lib.LIB_PATH))
+lib.pk_op_configs.argtypes = [C.c_char_p, C.c_longlong, C.c_longlong, C.c_longlong, C.c_void_p, C.c_int]
+lib.pk_op_default_config.argtypes = [C.c_char_p, C.c_longlong, C.c_longlong, C.c_longlong, C.POINTER(_lib.Config)]
+lib.pk_int8_default_config.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(_lib.Config)]
+for f in ("pk_mlp_block_workspace_size", "pk_decode_mlp_int8_workspace_size"):
+    getattr(lib, f).argtypes = [C.c_int, C.c_int, C.c_int]
+    getattr(lib, f).restype = C.c_size_t
+dims = [-1, 0, 1, 16, 64, 4096]
+ops = sys.argv[2].split(",")
+buf = (_lib.Config * 512)()
+for op, (m, n, k) in itertools.product(ops, itertools.product(dims, repeat=3)):
+    c = _lib.Config()
+    rc = lib.pk_op_default_config(op.encode(), m, n, k, C.byref(c))
+    cnt = lib.pk_op_configs(op.encode(), m, n, k, buf, 512)
+    if min(m, n, k) <= 0 and op.startswith(("matmul", "fused_matmul")):
+        assert rc != 0 and cnt == 0, (op, m, n, k, rc, cnt)
+for m, n, k in itertools.product(dims, repeat=3):
+    c = _lib.Config()
+    rc = lib.pk_int8_default_config(m, n, k, C.byref(c))
+    if min(m, n, k) <= 0:
+        assert rc != 0, (m, n, k)
+    for f in ("pk_mlp_block_workspace_size", "pk_decode_mlp_int8_workspace_size"):
+        v = getattr(lib, f)(m, n, k)
+        if min(m, n, k) <= 0:
+            assert v == 0, (f, m, n, k, v)
+        else:
+            assert v < (1 << 40), (f, m, n, k, v)
+print("ok")
+"""
+
+
+def _run_child(ops):
+    res = subprocess.run([sys.executable, "-c", _CHILD, str(ROOT), ",".join(ops)],
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), \
+        f"child exited {res.returncode}:\n{res.stdout[-2000:]}\n{res.stderr[-2000:]}"
+
+
+def test_degenerate_shapes_never_abort():
+    _run_child(OPS)
+
+
+def test_int8_zero_k_is_an_error_not_a_crash():
+    """pk_op_default_config('matmul_int8', 16, 64, 0) used to divide by a zero
+    split length inside the variant planner."""
+    import ctypes as C
+
+    from polykernel_amd import _lib
+
+    lib = C.CDLL(str(_lib.LIB_PATH))
+    lib.pk_op_default_config.argtypes = [C.c_char_p, C.c_longlong, C.c_longlong, C.c_longlong,
+                                         C.POINTER(_lib.Config)]
+    lib.pk_last_error.restype = C.c_char_p
+    c = _lib.Config()
+    assert lib.pk_op_default_config(b"matmul_int8", 16, 64, 0, C.byref(c)) == _lib.PK_ERR_UNSUPPORTED
+    assert b"no configuration" in lib.pk_last_error()
+    lib.pk_decode_mlp_int8_workspace_size.restype = C.c_size_t
+    assert lib.pk_decode_mlp_int8_workspace_size(1, 0, 64) == 0

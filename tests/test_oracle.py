@@ -56,6 +56,100 @@ def test_bf16_rne_matches_reference_helper(oracle, ref):
         assert oracle.lib().pko_f32_to_bf16(v) == ref.ref_f32_to_bf16(v)
 
 
+# ---------------------------------------------------------------- add / bias (golden.py:48-55)
+
+def _bf16_bits(exp: np.ndarray, man: np.ndarray, sign: np.ndarray) -> np.ndarray:
+    return ((sign.astype(np.uint32) << 15) | (exp.astype(np.uint32) << 7) | man.astype(np.uint32)).astype(np.uint16)
+
+
+def _independent_add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """bf16(f32(a) + f32(b)) by another route: the bf16 codes are widened by
+    torch, added by numpy's IEEE fp32 add, and rounded back by torch's RNE
+    conversion -- no line of the oracle is involved."""
+    import torch
+
+    fa = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).float().numpy()
+    fb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).float().numpy()
+    with np.errstate(over="ignore", invalid="ignore"):
+        s = (fa + fb).astype(np.float32)
+    return torch.from_numpy(s).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16), s
+
+
+def _add_sweep_pairs() -> tuple[np.ndarray, np.ndarray]:
+    """Structured operand pairs: every exponent-difference class 0..26 (exact,
+    one guard bit, ties, sticky bits, b below half an ulp of a), both relative
+    signs (carry-out and cancellation), all 128 x 128 mantissa pairs for a
+    normal exponent; subnormals, the largest finite values (overflow to inf),
+    +-0, +-inf and NaN; plus random code pairs."""
+    man = np.arange(128, dtype=np.uint32)
+    ma, mb = np.meshgrid(man, man, indexing="ij")
+    ma, mb = ma.reshape(-1), mb.reshape(-1)
+    A, B = [], []
+    for ea in (1, 100, 127, 200, 254):
+        for d in range(0, 27):
+            eb = ea - d
+            if eb < 0:
+                continue
+            for sb in (0, 1):
+                A.append(_bf16_bits(np.full_like(ma, ea), ma, np.zeros_like(ma)))
+                B.append(_bf16_bits(np.full_like(mb, eb), mb, np.full_like(mb, sb)))
+    # subnormal + subnormal and subnormal + smallest normals
+    sub = np.arange(1, 128, dtype=np.uint16)
+    sa, sb_ = np.meshgrid(sub, np.concatenate([sub, sub | 0x8000, sub + 0x80]), indexing="ij")
+    A.append(sa.reshape(-1).astype(np.uint16))
+    B.append(sb_.reshape(-1).astype(np.uint16))
+    specials = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0xFFC1, 0x7F81, 0x7F7F, 0xFF7F,
+                         0x3F80, 0xBF80, 0x0001, 0x8001], np.uint16)
+    xa, xb = np.meshgrid(specials, specials, indexing="ij")
+    A.append(xa.reshape(-1))
+    B.append(xb.reshape(-1))
+    r = np.random.default_rng(0xADD)
+    A.append(r.integers(0, 1 << 16, size=200000, dtype=np.uint32).astype(np.uint16))
+    B.append(r.integers(0, 1 << 16, size=200000, dtype=np.uint32).astype(np.uint16))
+    return np.concatenate(A), np.concatenate(B)
+
+
+def test_add_matches_independent_bf16_add(oracle):
+    """golden.add (tests/golden/golden.py:48-50) = bf16(f32(a) + f32(b)),
+    pinned against numpy fp32 addition + torch RNE, which share no code with
+    oracle.c.  A NaN sum must come back as a quiet NaN (the reference's NaN
+    rule keeps the payload; which operand's payload survives is the FPU's
+    choice, so only quietness is asserted)."""
+    a, b = _add_sweep_pairs()
+    got = oracle.add(a, b)
+    want, s = _independent_add(a, b)
+    nan = np.isnan(s)
+    assert nan.sum() > 0 and (~nan).sum() > 2_000_000
+    bad = np.flatnonzero(got[~nan] != want[~nan])
+    assert bad.size == 0, [(hex(a[~nan][i]), hex(b[~nan][i]), hex(got[~nan][i]), hex(want[~nan][i]))
+                           for i in bad[:8]]
+    g = got[nan]
+    assert np.all((g & 0x7FC0) == 0x7FC0), "NaN sums must be quiet NaNs"
+    # the sweep separates RNE from a plausible wrong rounding: truncating the
+    # fp32 sum instead would disagree on many pairs
+    trunc = ((s.view(np.uint32) >> 16).astype(np.uint16))
+    assert np.count_nonzero(trunc[~nan] != want[~nan]) > 1000
+
+
+def test_add_known_answers(oracle):
+    # exact, tie-to-even down / up, carry into the exponent, cancellation to +0,
+    # overflow to inf, inf - inf = NaN
+    a = bf([1.0, 1.0, 1.0, 255.0, 1.5, 3.3895314e38, np.inf])
+    b = bf([2.0, 2.0**-8, 3 * 2.0**-8, 1.0, -1.5, 3.3895314e38, -np.inf])
+    out = oracle.add(a, b)
+    assert list(out[:6]) == [0x4040, 0x3F80, 0x3F82, 0x4380, 0x0000, 0x7F80]
+    assert (out[6] & 0x7FC0) == 0x7FC0
+
+
+def test_bias_is_rowwise_add(oracle):
+    """golden.bias (golden.py:53-55) is the add above with the bias row
+    broadcast; checked against the independent add."""
+    x = rng_bf16((37, 129), 9, -4, 4)
+    b = rng_bf16((129,), 10, -4, 4)
+    want, _ = _independent_add(x.reshape(-1), np.broadcast_to(b, x.shape).reshape(-1).copy())
+    assert np.array_equal(oracle.bias(x, b), want.reshape(x.shape))
+
+
 # ---------------------------------------------------------------- known answers (test_golden_self.py)
 
 def test_known_matmul_2x2(oracle):

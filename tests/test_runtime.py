@@ -435,3 +435,21 @@ def test_hip_detector_without_gpu_reports_detection_failure():
         rt.Runtime(c).resolve(OP, SHAPE["M"], SHAPE["N"], SHAPE["K"])
     assert ei.value.code == _lib.PK_ERR_NO_DEVICE
     assert "device detection failed" in ei.value.message
+
+
+def test_code_object_int8_launcher_rejects_null_operands():
+    """The code-object int8 launcher refuses null operands before loading or
+    launching anything, with the linked path's wording (no GPU needed)."""
+    c = rt.KernelCache()
+    shape = dict(M=16, N=28672, K=8192, dtype="int8")
+    e = entry(op="matmul_int8_gelu", shape=shape)
+    e["best"] = {"block_m": 16, "block_n": 512, "block_k": 2048, "num_warps": 4,
+                 "vector_width": 16, "unroll": 2, "shared_memory_stages": 3}
+    c.put(e)
+    r = rt.Runtime(c, fixed_arch="gfx950", code_objects=True)
+    for missing in ("A", "Wq", "scale", "C"):
+        io = rt.MatmulInt8IO(A=16, Wq=16, scale=16, C=16, M=16, N=28672, K=8192)
+        setattr(io, missing, None)
+        with pytest.raises(rt.RuntimeError_) as ei:
+            r.run("matmul_int8_gelu", 16, 28672, 8192, io)
+        assert "null tensor pointer" in ei.value.message, ei.value.message
