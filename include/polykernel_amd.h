@@ -115,6 +115,21 @@ PK_API int launch_kv_cache_update(const uint16_t *cache, const uint16_t *new_row
 PK_API int launch_matmul_int8(const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C,
                        int M, int N, int K, void *stream);
 
+/* launch_matmul_int8 without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight decode/serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results (bit-identical) as
+ * launch_matmul_int8; the split-K partials live in a static 16 MiB device
+ * array of the library (one per GPU, held until the process ends) instead of
+ * the library workspace.  A shape whose split-K partials need more than
+ * 16 MiB returns PK_ERR_WORKSPACE without launching.  Calls allocate nothing
+ * (no hipMalloc / hipFree) and share the array: calls that overlap on one
+ * GPU -- on any streams, from any threads -- race on it and must be
+ * serialised by the caller.  pk_init() looks up the array's address for the
+ * current device; otherwise the first call on a device does. */
+PK_API int launch_matmul_int8_noalloc(const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C,
+                                      int M, int N, int K, void *stream);
+
 /* ---- fused ops the reference has only as golden compositions ----------- */
 
 /* out = rmsnorm(bf16(x + r), gamma, eps); gamma may be NULL.

@@ -71,6 +71,7 @@ SIGNATURES = {
     "launch_attention_prefill": (I, [P, P, P, P, I, I, I, I, I, F, I, P]),
     "launch_kv_cache_update": (I, [P, P, P, I, I, I, I, I, P]),
     "launch_matmul_int8": (I, [P, P, P, P, I, I, I, P]),
+    "launch_matmul_int8_noalloc": (I, [P, P, P, P, I, I, I, P]),
     "launch_fused_residual_rmsnorm": (I, [P, P, P, P, I, I, F, P]),
     "launch_fused_softmax_mask": (I, [P, P, P, I, I, P]),
     "launch_fused_rmsnorm_matmul_gamma": (I, [P, P, P, P, I, I, I, F, P]),

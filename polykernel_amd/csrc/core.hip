@@ -263,7 +263,9 @@ int pk_library_workspace(size_t bytes, void *stream, void **ptr) {
 
 int pk_init(void) {
   const uint16_t *t = nullptr;
-  return gelu_table(&t);
+  int rc = gelu_table(&t);
+  if (rc) return rc;
+  return int8_scratch_setup(nullptr);
 }
 
 int pk_check_bf16_conversion(unsigned long long *mismatches) {

@@ -21,6 +21,8 @@
 //     workspace and int8_reduce_kernel sums the splits in split order.
 // Epilogues: plain, GELU (exact table) and residual add, each with the
 // golden's per-stage bf16 rounding.
+#include <mutex>
+
 #include "int8_stream.hpp"
 
 namespace pk {
@@ -496,11 +498,68 @@ int int8_run(int epi, const uint16_t *A, const int8_t *W, const float *scale, ui
   return PK_OK;
 }
 
+// ---- the no-allocation variant of launch_matmul_int8 -------------------------
+// Split-K partials go to this file-scope device array instead of library or
+// caller memory.  Every GPU the library runs on holds its own copy (16 MiB)
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// not device memory: its device address is looked up per device with
+// hipGetSymbolAddress once (int8_scratch_setup) and only that address is
+// passed to kernels.
+constexpr size_t kInt8ScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) float scratch[kInt8ScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+// Device address of the current device's `scratch` (looked up on the first
+// call per device; later calls only read the table).
+int int8_scratch_setup(void **out) {
+  int dev = 0;
+  PK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kScratchDevices) {
+    set_error("device ordinal %d out of range", dev);
+    return PK_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  if (out) *out = g_scratch_ptr[dev];
+  return PK_OK;
+}
+
 }  // namespace pk
 
 using namespace pk;
 
 extern "C" {
+
+int launch_matmul_int8_noalloc(const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C, int M, int N,
+                               int K, void *stream) {
+  PK_CHECK_ARG(A && Wq && scale && C, "launch_matmul_int8_noalloc: null tensor pointer");
+  PK_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "launch_matmul_int8_noalloc: invalid shape M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return PK_OK;
+  const size_t need = int8_workspace_bytes(M, N, K);
+  if (need > kInt8ScratchBytes) {
+    set_error("launch_matmul_int8_noalloc: M=%d N=%d K=%d needs %zu bytes of split-K scratch, more than the %zu "
+              "of the static buffer; use launch_matmul_int8 or pk_matmul_int8_ex with a workspace",
+              M, N, K, need, kInt8ScratchBytes);
+    return PK_ERR_WORKSPACE;
+  }
+  void *ws = nullptr;
+  int rc = int8_scratch_setup(&ws);
+  if (rc) return rc;
+  // A caller workspace (the scratch) is never grown or replaced: int8_run
+  // allocates nothing when it is given one.
+  return int8_run(I8_NONE, A, Wq, scale, C, nullptr, M, N, K, nullptr, ws, kInt8ScratchBytes,
+                  (hipStream_t)stream);
+}
 
 int launch_matmul_int8(const uint16_t *A, const int8_t *Wq, const float *scale, uint16_t *C,
                        int M, int N, int K, void *stream) {

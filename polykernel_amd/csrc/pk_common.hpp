@@ -53,6 +53,9 @@ inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3
 // use.  Returns its device address for the current device (kernels take it as
 // an argument).
 int gelu_table(const uint16_t **table);
+// Device address (current device) of the static split-K scratch of
+// launch_matmul_int8_noalloc; looked up once per device.  `out` may be null.
+int int8_scratch_setup(void **out);
 
 // Configurations in the tuning-cache vocabulary (each defined beside the
 // dispatcher it describes).  *_configs write min(total, cap) entries and
