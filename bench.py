@@ -15,9 +15,13 @@ on the stream it runs on.
 
 value = 2^40 algorithmic FLOP per step / wall time per step (TFLOP/s).
 The other BASELINE configs (attention prefill, residual+RMSNorm, masked
-softmax, int8 decode, RMSNorm->MatMul) are reported under "extra", and the
-CPU oracle is timed on a bounded row sample under "cpu_baseline".
-One JSON line is printed.
+softmax, int8 decode, RMSNorm->MatMul) are reported under "extra", each with
+the CPU oracle timed on one thread and on all threads (a bounded sample,
+extrapolated per row / head where it is smaller than the workload) and the
+parity of the GPU output on that sample; the config-2 oracle timing is
+"cpu_baseline".  One JSON line is printed.
+
+    python bench.py --only cfg4a [--no-cpu]   # one config (for rocprofv3 runs)
 """
 from __future__ import annotations
 
@@ -134,30 +138,26 @@ def bench_mlp(steps: int, warmup: int):
     return elapsed, g1, g2, entry_ms, inputs, (entry1, entry2)
 
 
-def bench_extra(reps: int = 20):
-    """Other BASELINE configs after 3 warmup launches: the mean per launch of
-    `reps` back-to-back launches (HIP events around the batch), and the median
-    and minimum of `reps` launches timed one by one; config 1 also cold (a
-    1 GiB buffer written between launches, each launch timed alone)."""
-    import numpy as np
-    import torch
+class Timer:
+    """HIP-event timing on torch's current stream (the stream every launch
+    below is issued on)."""
 
-    from polykernel_amd import _lib, kernels, synth
-    from polykernel_amd import runtime as prt
-    from polykernel_amd._lib import check
+    def __init__(self, reps: int = 20):
+        import torch
 
-    lib = _lib.load()
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-    out = {}
+        self.reps = reps
+        self.stream = torch.cuda.current_stream()
+        self.sp = self.stream.cuda_stream
+        self.stats = {}
 
-    stats = {}
+    def __call__(self, fn, key=None, warm=3, flush=None):
+        """Mean per launch over `reps` back-to-back launches (the median of
+        three such batches; per-launch pairs of events when `flush` runs
+        between launches); with `key`, the median and minimum of `reps`
+        launches timed one by one go into stats[key]."""
+        import torch
 
-    def timeit(fn, n=reps, warm=3, key=None, flush=None):
-        """Mean per launch over n back-to-back launches (the median of three
-        such batches; per-launch pairs of events when `flush` runs between
-        launches); with `key`, the median and minimum of n launches timed one
-        by one go into stats[key]."""
+        n, stream = self.reps, self.stream
         for _ in range(warm):
             fn()
         evs = [event_pair() for _ in range(n)]
@@ -170,7 +170,7 @@ def bench_extra(reps: int = 20):
         torch.cuda.synchronize()
         t = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
         if key:
-            stats[key] = {"median_us": round(t[n // 2] * 1e3, 2), "min_us": round(t[0] * 1e3, 2)}
+            self.stats[key] = {"median_us": round(t[n // 2] * 1e3, 2), "min_us": round(t[0] * 1e3, 2)}
         if flush is not None:
             return sum(t) / n
         # three batches of n back-to-back launches, the median batch mean: per-launch
@@ -186,68 +186,231 @@ def bench_extra(reps: int = 20):
             means.append(e0.elapsed_time(e1) / n)
         return sorted(means)[1]
 
-    # config 1: RMSNorm -> MatMul fragment (cache-resident)
-    x = dev_bf16(synth.normal_bf16((128, 768), 11))
-    g = dev_bf16(synth.normal_bf16((768,), 12, 0.1, 1.0))
-    w = dev_bf16(synth.normal_bf16((768, 3072), 13, 1 / math.sqrt(768)))
-    o = torch.empty(128, 3072, dtype=torch.bfloat16, device="cuda")
-    cfg1 = lambda: check(lib.launch_fused_rmsnorm_matmul_gamma(
-        x.data_ptr(), g.data_ptr(), w.data_ptr(), o.data_ptr(), 128, 3072, 768, 1e-6, sp), "cfg1")
-    ms = timeit(cfg1, key="warm")
-    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
-    ms_cold = timeit(cfg1, key="cold", flush=lambda: big.fill_(1))
-    out["rmsnorm_matmul_cfg1"] = {"us": round(ms * 1e3, 2),
-                                  "tflops": round(2 * 128 * 3072 * 768 / (ms * 1e-3) / 1e12, 2),
-                                  "warm": stats["warm"], "cold_us": round(ms_cold * 1e3, 2), "cold": stats["cold"],
-                                  "note": "warm: L2/MALL-resident (5.7 MB); cold: a 1 GiB buffer written between launches"}
-    del x, g, w, o, big
 
-    # config 3: KV append (in place) + causal prefill, B1 H32 D128, 3584 + 512
+def host_info() -> dict:
+    """The host the CPU baselines ran on: usable cores and CPU model."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"nproc": usable, "cpu_model": model}
+
+
+def cpu_pair(run, single_sample, all_sample, unit: str, work_per_unit: float, total_units: float,
+             what: str) -> dict:
+    """Time the oracle (the C restatement of kernels/cpu) on one thread and on
+    every thread OpenMP gives it: run(sample) processes `sample` units (rows,
+    queries, ...) of the workload, `work_per_unit` is the metric's work (FLOP
+    or algorithmic bytes) per unit, extrapolated to `total_units` when the
+    sample is smaller than the workload."""
+    from oracle import pyoracle
+
+    threads = pyoracle.num_threads()
+    res = {}
+    for name, sample, nthr in (("single_thread", single_sample, 1), ("all_cores", all_sample, threads)):
+        pyoracle.set_num_threads(nthr)
+        try:
+            t0 = time.perf_counter()
+            out = run(sample)
+            dt = time.perf_counter() - t0
+        finally:
+            pyoracle.set_num_threads(threads)
+        scale = 1e12 if unit == "TFLOP/s" else 1e9
+        res[name] = {"value": round(sample * work_per_unit / dt / scale, 6), "unit": unit, "cores": nthr,
+                     "kind": "port", "seconds": round(dt, 3),
+                     "sample": f"{sample:g} of {total_units:g} {what}" +
+                               (" (extrapolated per unit)" if sample < total_units else " (full workload)")}
+        res.setdefault("_outputs", {})[name] = out
+    return res
+
+
+def _parity(got_bits, want_bits) -> dict:
+    from polykernel_amd import metrics
+
+    rep = metrics.report(got_bits, want_bits)
+    return {"cosine": round(rep.cosine, 7), "pcc": round(rep.pcc, 7), "max_rel_err": float(f"{rep.max_rel_err:.3e}"),
+            "bit_exact": round(rep.bit_exact, 6), "max_ulp": rep.max_ulp}
+
+
+def _finish_cpu(entry: dict, cpu: dict, gpu_bits, ref_of) -> None:
+    """Attach the CPU timings and the parity of the GPU output on the oracle's
+    all-cores sample (ref_of maps the oracle output onto the GPU slice)."""
+    outs = cpu.pop("_outputs")
+    entry["cpu_baseline"] = cpu
+    want, got = ref_of(outs["all_cores"], gpu_bits)
+    entry["parity_sample"] = _parity(got, want)
+
+
+def from_dev_bits(t):
+    import numpy as np
+    import torch
+
+    t = t.detach().cpu()
+    return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+
+def bench_cfg1(t: Timer, cpu: bool) -> dict:
+    """Config 1: RMSNorm -> MatMul fragment (cache-resident), warm and cold."""
+    import torch
+
+    from polykernel_amd import _lib, synth
+    from polykernel_amd._lib import check
+
+    lib = _lib.load()
+    hx = synth.normal_bf16((128, 768), 11)
+    hg = synth.normal_bf16((768,), 12, 0.1, 1.0)
+    hw = synth.normal_bf16((768, 3072), 13, 1 / math.sqrt(768))
+    x, g, w = dev_bf16(hx), dev_bf16(hg), dev_bf16(hw)
+    o = torch.empty(128, 3072, dtype=torch.bfloat16, device="cuda")
+    run = lambda: check(lib.launch_fused_rmsnorm_matmul_gamma(
+        x.data_ptr(), g.data_ptr(), w.data_ptr(), o.data_ptr(), 128, 3072, 768, 1e-6, t.sp), "cfg1")
+    ms = t(run, key="warm")
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    ms_cold = t(run, key="cold", flush=lambda: big.fill_(1))
+    flop = 2 * 128 * 3072 * 768
+    out = {"us": round(ms * 1e3, 2), "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+           "warm": t.stats["warm"], "cold_us": round(ms_cold * 1e3, 2), "cold": t.stats["cold"],
+           "note": "warm: L2/MALL-resident (5.7 MB); cold: a 1 GiB buffer written between launches"}
+    del big
+    if cpu:
+        from oracle import pyoracle
+
+        c = cpu_pair(lambda n: pyoracle.fused_rmsnorm_matmul(hx, hw, hg, 1e-6), 128, 128, "TFLOP/s",
+                     flop / 128, 128, "rows of x [128,768] @ W [768,3072]")
+        _finish_cpu(out, c, from_dev_bits(o), lambda want, got: (want, got))
+    return out
+
+
+def _cfg3_inputs():
+    from polykernel_amd import synth
+
     B, H, Sc, Sn, Dh = 1, 32, 3584, 512, 128
-    q = dev_bf16(synth.normal_bf16((B, H, Sn, Dh), 21))
-    kn = dev_bf16(synth.normal_bf16((B, H, Sn, Dh), 22))
-    vn = dev_bf16(synth.normal_bf16((B, H, Sn, Dh), 23))
+    return dict(B=B, H=H, Sc=Sc, Sn=Sn, Dh=Dh,
+                q=synth.normal_bf16((B, H, Sn, Dh), 21), kn=synth.normal_bf16((B, H, Sn, Dh), 22),
+                vn=synth.normal_bf16((B, H, Sn, Dh), 23), kc=synth.normal_bf16((B, H, Sc, Dh), 24),
+                vc=synth.normal_bf16((B, H, Sc, Dh), 25))
+
+
+CFG3_FLOP = 32216449024   # 4 * D per unmasked (query, key) pair
+
+
+def bench_cfg3(t: Timer, cpu: bool) -> dict:
+    """Config 3: KV append (in place) + causal prefill, B1 H32 D128, 3584 + 512."""
+    import numpy as np
+    import torch
+
+    from polykernel_amd import _lib
+    from polykernel_amd._lib import check
+
+    lib = _lib.load()
+    h = _cfg3_inputs()
+    B, H, Sc, Sn, Dh = h["B"], h["H"], h["Sc"], h["Sn"], h["Dh"]
+    scale = 1 / math.sqrt(Dh)
+    q, kn, vn = dev_bf16(h["q"]), dev_bf16(h["kn"]), dev_bf16(h["vn"])
     kc = torch.empty(B, H, Sc + Sn, Dh, dtype=torch.bfloat16, device="cuda")
     vc = torch.empty_like(kc)
-    kc[:, :, :Sc] = dev_bf16(synth.normal_bf16((B, H, Sc, Dh), 24))
-    vc[:, :, :Sc] = dev_bf16(synth.normal_bf16((B, H, Sc, Dh), 25))
+    kc[:, :, :Sc] = dev_bf16(h["kc"])
+    vc[:, :, :Sc] = dev_bf16(h["vc"])
     o = torch.empty_like(q)
-    ms = timeit(lambda: check(lib.launch_fused_kv_append_attention(
+    ms = t(lambda: check(lib.launch_fused_kv_append_attention(
         q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kn.data_ptr(), vn.data_ptr(), o.data_ptr(),
-        B, H, Sn, Sc, Dh, Sc + Sn, 1 / math.sqrt(Dh), 1, sp), "cfg3"), key="cfg3")
-    flop = 32216449024
-    tf = flop / (ms * 1e-3) / 1e12
-    out["attention_prefill_cfg3"] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                                     "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4), **stats["cfg3"]}
-    del q, kn, vn, kc, vc, o
+        B, H, Sn, Sc, Dh, Sc + Sn, scale, 1, t.sp), "cfg3"), key="cfg3")
+    tf = CFG3_FLOP / (ms * 1e-3) / 1e12
+    out = {"us": round(ms * 1e3, 2), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4),
+           **t.stats["cfg3"]}
+    if cpu:
+        from oracle import pyoracle
 
-    # config 4a: residual + RMSNorm [16384, 8192]
+        kfull = np.concatenate([h["kc"], h["kn"]], axis=2)
+        vfull = np.concatenate([h["vc"], h["vn"]], axis=2)
+        # heads are independent and equal work: time whole heads
+        run = lambda nh: pyoracle.attention_prefill(h["q"][:, :nh], kfull[:, :nh], vfull[:, :nh], scale, True)
+        c = cpu_pair(run, 1, 16, "TFLOP/s", CFG3_FLOP / H, H, "heads (all 512 queries, 4096 keys each)")
+        _finish_cpu(out, c, from_dev_bits(o), lambda want, got: (want, got[:, :want.shape[1]]))
+    return out
+
+
+def bench_cfg4a(t: Timer, cpu: bool) -> dict:
+    """Config 4a: residual + RMSNorm [16384, 8192]."""
+    import torch
+
+    from polykernel_amd import _lib, synth
+    from polykernel_amd._lib import check
+
+    lib = _lib.load()
     R, C = 16384, 8192
-    xa = dev_bf16(synth.normal_bf16((R, C), 31))
-    ra = dev_bf16(synth.normal_bf16((R, C), 32))
-    ga = dev_bf16(synth.normal_bf16((C,), 33, 0.1, 1.0))
+    hx, hr = synth.normal_bf16((R, C), 31), synth.normal_bf16((R, C), 32)
+    hg = synth.normal_bf16((C,), 33, 0.1, 1.0)
+    xa, ra, ga = dev_bf16(hx), dev_bf16(hr), dev_bf16(hg)
     oa = torch.empty_like(xa)
-    ms = timeit(lambda: check(lib.launch_fused_residual_rmsnorm(
-        xa.data_ptr(), ra.data_ptr(), ga.data_ptr(), oa.data_ptr(), R, C, 1e-6, sp), "cfg4a"), key="cfg4a")
-    gbs = 805322752 / (ms * 1e-3) / 1e9
-    out["residual_rmsnorm_cfg4a"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
-                                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), **stats["cfg4a"]}
-    del xa, ra, ga, oa
+    ms = t(lambda: check(lib.launch_fused_residual_rmsnorm(
+        xa.data_ptr(), ra.data_ptr(), ga.data_ptr(), oa.data_ptr(), R, C, 1e-6, t.sp), "cfg4a"), key="cfg4a")
+    nbytes = 805322752
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+           **t.stats["cfg4a"]}
+    if cpu:
+        from oracle import pyoracle
 
-    # config 4b: masked softmax fp32 logits [16384, 8192] + bf16 additive mask
-    lg = torch.from_numpy(synth.normal_f32((R, C), 34, 2.0)).cuda()
-    mk = dev_bf16(synth.mask_bf16((R, C), 35, 0.1))
+        run = lambda n: pyoracle.residual_rmsnorm(hx[:n], hr[:n], hg, 1e-6)
+        c = cpu_pair(run, 2048, R, "GB/s", nbytes / R, R, "rows of [16384,8192]")
+        _finish_cpu(out, c, from_dev_bits(oa), lambda want, got: (want, got))
+    return out
+
+
+def bench_cfg4b(t: Timer, cpu: bool) -> dict:
+    """Config 4b: masked softmax, fp32 logits [16384, 8192] + bf16 additive mask."""
+    import torch
+
+    from polykernel_amd import _lib, synth
+    from polykernel_amd._lib import check
+
+    lib = _lib.load()
+    R, C = 16384, 8192
+    hl, hm = synth.normal_f32((R, C), 34, 2.0), synth.mask_bf16((R, C), 35, 0.1)
+    lg, mk = torch.from_numpy(hl).cuda(), dev_bf16(hm)
     om = torch.empty(R, C, dtype=torch.bfloat16, device="cuda")
-    ms = timeit(lambda: check(lib.launch_fused_softmax_mask(lg.data_ptr(), mk.data_ptr(), om.data_ptr(),
-                                                            R, C, sp), "cfg4b"), key="cfg4b")
-    gbs = 1073741824 / (ms * 1e-3) / 1e9
-    out["masked_softmax_cfg4b"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
-                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), **stats["cfg4b"]}
-    del lg, mk, om
+    ms = t(lambda: check(lib.launch_fused_softmax_mask(lg.data_ptr(), mk.data_ptr(), om.data_ptr(), R, C, t.sp),
+                         "cfg4b"), key="cfg4b")
+    nbytes = 1073741824
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+           **t.stats["cfg4b"]}
+    if cpu:
+        from oracle import pyoracle
 
-    # config 5: int8 decode MLP, M=16, 8192 <-> 28672 (weights quantised on the GPU)
+        run = lambda n: pyoracle.softmax_mask(hl[:n], hm[:n])
+        c = cpu_pair(run, 1024, R, "GB/s", nbytes / R, R, "rows of [16384,8192]")
+        _finish_cpu(out, c, from_dev_bits(om), lambda want, got: (want, got))
+    return out
+
+
+CFG5_BYTES = 470433792
+
+
+def bench_cfg5(t: Timer, cpu: bool) -> dict:
+    """Config 5: int8 decode MLP, M=16, 8192 <-> 28672 (weights quantised on the
+    GPU); the runtime-served tuned configs over two weight copies used in turn,
+    and the library's launch_decode_mlp_int8 beside it."""
+    import torch
+
+    from polykernel_amd import _lib, kernels, synth
+    from polykernel_amd import runtime as prt
+    from polykernel_amd._lib import check
+
+    lib = _lib.load()
+    sp = t.sp
     Md, dd, Fd = 16, 8192, 28672
-    xd = dev_bf16(synth.normal_bf16((Md, dd), 41))
+    hx = synth.normal_bf16((Md, dd), 41)
+    xd = dev_bf16(hx)
     w1q, s1 = kernels.quantize_per_channel(dev_bf16(synth.normal_bf16((dd, Fd), 42, 1 / math.sqrt(dd))))
     w2q, s2 = kernels.quantize_per_channel(dev_bf16(synth.normal_bf16((Fd, dd), 43, 1 / math.sqrt(Fd))))
     torch.cuda.empty_cache()
@@ -265,8 +428,7 @@ def bench_extra(reps: int = 20):
             xd.data_ptr(), a.data_ptr(), s1.data_ptr(), b.data_ptr(), s2.data_ptr(), od.data_ptr(),
             Md, dd, Fd, ws.data_ptr(), ws.numel(), sp), "cfg5")
 
-    ms_entry = timeit(decode)
-    # the same chain served by the runtime with the tuned configs
+    ms_entry = t(decode)
     served = prt.default_runtime()
     hd = torch.empty(Md, Fd, dtype=torch.bfloat16, device="cuda")
     ios = []
@@ -284,14 +446,42 @@ def bench_extra(reps: int = 20):
         served.run("matmul_int8_gelu", Md, Fd, dd, i1)
         served.run("matmul_int8_residual", Md, dd, Fd, i2)
 
-    ms = timeit(decode_served, key="cfg5")
-    gbs = 470433792 / (ms * 1e-3) / 1e9
-    out["int8_decode_mlp_cfg5"] = {
-        "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), **stats["cfg5"],
-        "launch_decode_mlp_int8_us": round(ms_entry * 1e3, 2),
-        "served_configs": [served.resolve("matmul_int8_gelu", Md, Fd, dd)["best"],
-                           served.resolve("matmul_int8_residual", Md, dd, Fd)["best"]],
-        "note": "runtime-served tuned configs; 2 weight copies in turn (no MALL reuse)"}
+    ms = t(decode_served, key="cfg5")
+    gbs = CFG5_BYTES / (ms * 1e-3) / 1e9
+    out = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+           **t.stats["cfg5"], "launch_decode_mlp_int8_us": round(ms_entry * 1e3, 2),
+           "served_configs": [served.resolve("matmul_int8_gelu", Md, Fd, dd)["best"],
+                              served.resolve("matmul_int8_residual", Md, dd, Fd)["best"]],
+           "note": "runtime-served tuned configs; 2 weight copies in turn (no MALL reuse)"}
+    if cpu:
+        from oracle import pyoracle
+
+        torch.cuda.synchronize()
+        hw1, hs1, hw2, hs2 = (from_dev_bits(v) for v in (w1q, s1, w2q, s2))
+        run = lambda n: pyoracle.decode_mlp_int8(hx[:n], hw1, hs1, hw2, hs2)
+        # rows of x are independent: each row streams every weight once
+        c = cpu_pair(run, 1, Md, "GB/s", CFG5_BYTES / Md, Md, "rows of x [16,8192] through W1 and W2")
+        _finish_cpu(out, c, from_dev_bits(od), lambda want, got: (want, got))
+    return out
+
+
+EXTRA = {"cfg1": ("rmsnorm_matmul_cfg1", bench_cfg1), "cfg3": ("attention_prefill_cfg3", bench_cfg3),
+         "cfg4a": ("residual_rmsnorm_cfg4a", bench_cfg4a), "cfg4b": ("masked_softmax_cfg4b", bench_cfg4b),
+         "cfg5": ("int8_decode_mlp_cfg5", bench_cfg5)}
+
+
+def bench_extra(cpu: bool, only=None, reps: int = 20) -> dict:
+    """The other BASELINE configs: GPU time per launch (Timer), and with `cpu`
+    the oracle on one thread and on all threads plus the parity of the GPU
+    output on the oracle's sample."""
+    import torch
+
+    out = {}
+    for name, (key, fn) in EXTRA.items():
+        if only and name != only:
+            continue
+        out[key] = fn(Timer(reps), cpu)
+        torch.cuda.empty_cache()
     return out
 
 
@@ -363,7 +553,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
+    ap.add_argument("--only", choices=sorted(EXTRA), default=None,
+                    help="run only this config (GPU timing; CPU baseline unless --no-cpu) and print its "
+                         "results -- the profiling entry point for one kernel family")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 1 GiB device-to-device copy (HBM ceiling and the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -399,6 +592,10 @@ def main() -> int:
 
     _lib.load()
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.only:
+        res = bench_extra(cpu=not args.no_cpu, only=args.only)
+        print(json.dumps({"only": args.only, "host": host_info(), **res}), flush=True)
+        return 0
     elapsed, g1, g2, entry_ms, inputs, entries = bench_mlp(args.steps, args.warmup)
     ms_step = elapsed / args.steps * 1e3
     value = MLP_FLOP / (ms_step * 1e-3) / 1e12
@@ -406,9 +603,9 @@ def main() -> int:
     g2_ms = sum(g2) / len(g2)
     achieved = GEMM_FLOP / (g1_ms * 1e-3) / 1e12
     log(f"mlp step {ms_step:.3f} ms -> {value:.1f} TFLOP/s; gemm1 {g1_ms:.3f} ms, gemm2 {g2_ms:.3f} ms")
-    extra = {}
+    extra = {"host": host_info()}
     if not args.no_extra:
-        extra = bench_extra()
+        extra.update(bench_extra(cpu=not args.no_cpu))
         log(f"extra: {json.dumps(extra)}")
     extra["mlp_block_breakdown"] = {
         "gemm1_bias_gelu_ms": round(g1_ms, 4), "gemm2_bias_residual_ms": round(g2_ms, 4),
@@ -419,6 +616,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(inputs)
+        cpu["cpu_model"] = extra["host"]["cpu_model"]
         log(f"cpu baseline: {cpu}")
         extra["cpu_baseline_single_thread"] = cpu_baseline_single(inputs)
         log(f"cpu baseline, one thread: {extra['cpu_baseline_single_thread']}")
