@@ -19,7 +19,7 @@
 // that key order, so P never leaves registers and the rescale by
 // exp(m_old - m_new) is a per-lane multiply.
 //
-// Work split (attention_kernel, any D <= 128): a workgroup = 4 waves x 32
+// Work split (attention_kernel, any D <= 256): a workgroup = 4 waves x 32
 // queries of one (b,h); K/V tiles are double-buffered in LDS.  When queries
 // alone do not fill the chip the key range is split (flash-decoding style)
 // and att_combine_kernel merges the fp32 partials in split order.  Head dims
@@ -200,9 +200,18 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttArgs g) {
     store_kv(0);
   }
   __syncthreads();
+  // The next tile is staged through registers.  Up to D = 128 its loads stay
+  // in flight during this tile's products (stored to LDS at the end); at
+  // D = 256 the accumulators and Q fragments fill the register file, so the
+  // next tile is loaded and stored at once, into the buffer no one reads in
+  // this iteration.
+  constexpr bool kOverlapLoads = DP <= 128;
   for (int t = t_begin; t < t_end; ++t) {
     const int cur = (t - t_begin) & 1;
-    if (t + 1 < t_end) load_kv(t + 1);
+    if (t + 1 < t_end) {
+      load_kv(t + 1);
+      if constexpr (!kOverlapLoads) store_kv(cur ^ 1);
+    }
     const uint16_t *ks = Ks[cur];
     const uint16_t *vs = Vs[cur];
     const int k0 = t * AT_BKV;
@@ -288,7 +297,8 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttArgs g) {
         acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb_lo, acc_o[db], 0, 0, 0);
       }
     }
-    if (t + 1 < t_end) store_kv(cur ^ 1);
+    if constexpr (kOverlapLoads)
+      if (t + 1 < t_end) store_kv(cur ^ 1);
     __syncthreads();
   }
 
@@ -933,12 +943,12 @@ pk_config fa_config(int qg, int D) {
   return pk_config{fa_bq(qg), fa_bkv(qg), D, FA_WAVES, 8, D / 16, FA_RING / (2 * fa_bkv(qg) * D * 2)};
 }
 bool generic_attention_config(int D, pk_config *out) {
-  const int dp = D <= 32 ? 32 : D <= 64 ? 64 : 128;
+  const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
   *out = pk_config{AT_BQ, AT_BKV, dp, AT_WAVES, D % 8 == 0 ? 8 : 1, dp / 16, 1};
   return true;
 }
 int attention_configs(int S_q, int S_kv, int D, pk_config *out, int cap) {
-  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 128) return 0;
+  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 256) return 0;
   pk_config c[2];
   int n = 0;
   if (D == 64 || D == 128) {
@@ -953,7 +963,7 @@ int attention_configs(int S_q, int S_kv, int D, pk_config *out, int cap) {
 // The built-in choice.  The shape key has no batch x heads: this assumes 32
 // (the headline configuration's and the autotuner's default).
 bool attention_config(int S_q, int S_kv, int D, pk_config *out) {
-  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 128) return false;
+  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 256) return false;
   if (D == 64 || D == 128) *out = fa_config(fa_default_qg(32, S_q), D);
   else generic_attention_config(D, out);
   return true;
@@ -993,7 +1003,8 @@ int attention_run(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint1
   if (D <= 32) return attention_dp<32>(g, st);
   if (D <= 64) return attention_dp<64>(g, st);
   if (D <= 128) return attention_dp<128>(g, st);
-  set_error("attention: head dim %d > 128 is not supported", D);
+  if (D <= 256) return attention_dp<256>(g, st);
+  set_error("attention: head dim %d > 256 is not supported", D);
   return PK_ERR_UNSUPPORTED;
 }
 
@@ -1007,6 +1018,10 @@ int fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc, con
   PK_CHECK_ARG((int64_t)S_cache + S_q <= cache_capacity,
                "launch_fused_kv_append_attention: S_cache + S_q = %lld exceeds cache_capacity %d",
                (long long)S_cache + S_q, cache_capacity);
+  if (D > 256) {  // refused before the append touches the caches
+    set_error("launch_fused_kv_append_attention: head dim %d > 256 is not supported", D);
+    return PK_ERR_UNSUPPORTED;
+  }
   const int64_t BH = (int64_t)B * H;
   if (BH == 0) return PK_OK;
   const int S_kv = S_cache + S_q;

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void naive_softmax_mask_kernel(const floa
   for (int c = 0; c < cols; ++c) y[base + c] = (uint16_t)f2bf(__fmul_rn(expf(__fsub_rn(z(c), m)), inv));
 }
 
-constexpr int kMaxD = 128;
+constexpr int kMaxD = 256;
 
 __global__ __launch_bounds__(64) void naive_attention_kernel(const uint16_t *__restrict__ Q,
                                                              const uint16_t *__restrict__ K,

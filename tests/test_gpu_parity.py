@@ -55,6 +55,46 @@ def _abs_dot(a_bits, b_bits):
     return np.abs(f32(a_bits).astype(np.float64)) @ np.abs(f32(b_bits).astype(np.float64))
 
 
+def _gate_bad(epi, a, b, got, bias=None, r=None, operand_ulps=0.0):
+    """Outputs outside the device fp32 error model (pk_gate_matmul): got must be
+    the reference epilogue (bf16 GEMM epi 0 none, 1 bias+GELU, 2 bias+residual)
+    applied to some fp32 accumulation of a @ b's products.  Arguments are
+    device tensors (a row sample of A, R and got is enough: rows are
+    independent)."""
+    import ctypes
+
+    import torch
+
+    from polykernel_amd import _lib
+
+    n = ctypes.c_ulonglong(0)
+    M, Kd = a.shape
+    N = b.shape[1]
+    ptr = lambda t: None if t is None else t.data_ptr()
+    _lib.check(_lib.load().pk_gate_matmul(epi, ptr(a), ptr(b), ptr(bias), ptr(r), ptr(got), M, N, Kd,
+                                          float(operand_ulps), ctypes.byref(n),
+                                          torch.cuda.current_stream().cuda_stream), "pk_gate_matmul")
+    return n.value
+
+
+def _gate_int8_bad(epi, a, wq, s, got, r=None):
+    """As _gate_bad for the int8 weight-only GEMM (epi 0 none, 1 GELU, 2 residual)."""
+    import ctypes
+
+    import torch
+
+    from polykernel_amd import _lib
+
+    n = ctypes.c_ulonglong(0)
+    M, Kd = a.shape
+    N = wq.shape[1]
+    _lib.check(_lib.load().pk_gate_matmul_int8(epi, a.data_ptr(), wq.data_ptr(), s.data_ptr(),
+                                               None if r is None else r.data_ptr(), got.data_ptr(), M, N, Kd,
+                                               ctypes.byref(n), torch.cuda.current_stream().cuda_stream),
+               "pk_gate_matmul_int8")
+    return n.value
+
+
 # ------------------------------------------------------------------ elementwise / rows
 
 def test_device_bf16_conversion_exhaustive(gpu):
@@ -244,11 +284,16 @@ def test_fused_matmul_bias_gelu(gpu, oracle, M, N, Kd):
     a = synth.normal_bf16((M, Kd), 26)
     b = synth.normal_bf16((Kd, N), 27, 1.0 / np.sqrt(Kd))
     bias = synth.normal_bf16((N,), 28, 0.02)
-    got = from_dev(K().fused_matmul_bias_gelu(to_dev(a), to_dev(b), to_dev(bias)))
+    da, db, dbias = to_dev(a), to_dev(b), to_dev(bias)
+    dgot = K().fused_matmul_bias_gelu(da, db, dbias)
+    got = from_dev(dgot)
     want = oracle.fused_matmul_bias_gelu(a, b, bias)
     rep = mt.report(got, want)
     assert rep.cosine >= 0.999 and rep.pcc >= 0.99, rep
     assert rep.bit_exact >= 0.95, rep
+    # every output is GELU(bf16(bf16(t) + bias)) for an fp32 accumulation t of the products
+    assert _gate_bad(1, da, db, dgot, bias=dbias) == 0, rep
+    assert _gate_bad(1, da, db, to_dev(want), bias=dbias) == 0  # the oracle's own order passes too
 
 
 @pytest.mark.parametrize("tile", [0, 3])
@@ -302,6 +347,33 @@ def test_mlp_block_config2_row_sample(gpu, oracle):
     rep = mt.report(got[rows], want)
     _say(f"mlp config2 sample: {rep}")
     assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+
+
+def test_mlp_block_config2_stages_error_model(gpu, oracle):
+    """Config 2 stage by stage at full size: RMSNorm, GEMM1 + bias + GELU,
+    GEMM2 + bias + residual, each GEMM checked on a row sample against the fp32
+    error model given the GPU's own previous stage (pk_gate_matmul: every
+    output is the reference epilogue of some fp32 accumulation of its
+    products); the stages chained give launch_mlp_block's bits."""
+    import torch
+
+    M, d, F = 4096, 4096, 16384
+    _say("mlp config2 stages")
+    x, g, w1, b1, w2, b2 = _mlp_inputs(M, d, F)
+    dx, dg, dw1, db1, dw2, db2 = map(to_dev, (x, g, w1, b1, w2, b2))
+    a = K().rmsnorm(dx, dg, 1e-6)
+    h = K().fused_matmul_bias_gelu(a, dw1, db1)
+    y = K().fused_matmul_bias_residual(h, dw2, db2, dx)
+    block = K().mlp_block(dx, dg, dw1, db1, dw2, db2, eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(block.view(torch.int16), y.view(torch.int16))
+    rows = torch.from_numpy(np.sort(np.random.default_rng(47).choice(M, 16, replace=False))).cuda()
+    pick = lambda t: t.index_select(0, rows).contiguous()
+    ra = from_dev(pick(a))
+    rep = mt.report(ra, oracle.rmsnorm(x[rows.cpu().numpy()], g, 1e-6))
+    assert rep.bit_exact >= 0.99 and rep.max_ulp <= 1, rep
+    assert _gate_bad(1, pick(a), dw1, pick(h), bias=db1) == 0
+    assert _gate_bad(2, pick(h), dw2, pick(y), bias=db2, r=pick(dx)) == 0
 
 
 # ------------------------------------------------------------------ int8
@@ -417,6 +489,13 @@ def test_decode_mlp_int8_config5(gpu, oracle):
     rep = mt.report(got, want)
     _say(f"decode config5: {rep}")
     assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+    # stage by stage against the fp32 error model given the GPU's own h
+    dx = to_dev(x)
+    h = K().matmul_int8_ex(1, dx, w1q, s1)
+    y = K().matmul_int8_ex(2, h, w2q, s2, residual=dx)
+    assert np.array_equal(from_dev(y), got)  # the chain is launch_decode_mlp_int8's
+    assert _gate_int8_bad(1, dx, w1q, s1, h) == 0
+    assert _gate_int8_bad(2, h, w2q, s2, y, r=dx) == 0
 
 
 # ------------------------------------------------------------------ attention
@@ -474,7 +553,33 @@ def test_attention_prefill_flash_path(gpu, oracle, B, H, Sq, Skv, D, causal):
     assert _att_bound_bad(oracle, got, want, q, k, v, causal) == 0, rep
 
 
-@pytest.mark.parametrize("Sc,D", [(192, 128), (201, 128), (128, 64), (130, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 2, 100, 300, 256), (2, 2, 64, 200, 200), (1, 1, 33, 70, 190),
+                                          (1, 1, 32, 2048, 256), (1, 3, 130, 130, 160)])
+def test_attention_prefill_wide_heads(gpu, oracle, B, H, Sq, Skv, D, causal):
+    """Head dims above 128 up to 256 (the generic kernel at DP = 256): aligned
+    and unaligned D, ragged tiles, and a one-tile grid whose key range is
+    split and merged."""
+    _say(f"attention wide {B},{H},{Sq},{Skv},{D} causal={causal}")
+    q, k, v = rng_bf16((B, H, Sq, D), 76), rng_bf16((B, H, Skv, D), 77), rng_bf16((B, H, Skv, D), 78)
+    got = from_dev(K().attention_prefill(to_dev(q), to_dev(k), to_dev(v), None, causal))
+    want = oracle.attention_prefill(q, k, v, None, causal)
+    rep = mt.report(got, want)
+    _say(f"attention wide: {rep}")
+    assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+    assert _att_bound_bad(oracle, got, want, q, k, v, causal) == 0, rep
+
+
+def test_attention_head_dim_above_256_refused(gpu):
+    from polykernel_amd._lib import PK_ERR_UNSUPPORTED, PolyKernelError
+
+    q = to_dev(rng_bf16((1, 1, 8, 264), 79))
+    with pytest.raises(PolyKernelError) as e:
+        K().attention_prefill(q, q, q, None, True)
+    assert e.value.code == PK_ERR_UNSUPPORTED and "256" in e.value.message
+
+
+@pytest.mark.parametrize("Sc,D", [(192, 128), (201, 128), (128, 64), (130, 64), (160, 256)])
 def test_fused_kv_append_attention_flash_path(gpu, oracle, Sc, D):
     """In-place append fused into the flash kernel (S_cache a multiple of its
     64-key step) and the fallback (separate append kernels) otherwise; the
