@@ -379,8 +379,10 @@ using KvAppendAttentionIO = pk_kv_append_attention_io;
 // config is one the kernels implement, then launches through the C-ABI.
 PK_API void RegisterBuiltinLaunchers(Runtime &runtime);
 
-// Serve matmul_int8, matmul_int8_gelu and matmul_int8_residual from the code
-// objects `cache` holds for their entries (codegen::EmitCodeObject): the
+// Serve the GEMM family (matmul, fused_matmul_bias_gelu,
+// fused_matmul_bias_residual) and matmul_int8, matmul_int8_gelu and
+// matmul_int8_residual from the code objects `cache` holds for their entries
+// (codegen::EmitCodeObject): the
 // object is loaded once (hash-checked) and launched with
 // hipModuleLaunchKernel.  An entry without a cached code object is an error.
 // `cache` must outlive the runtime.

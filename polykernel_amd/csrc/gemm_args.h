@@ -1,0 +1,19 @@
+/* gemm_args.h -- kernel arguments of the bf16 GEMM kernels, one layout for the
+ * device code (gemm_kernels.hpp) and for hosts that launch an emitted code
+ * object with hipModuleLaunchKernel (csrc/runtime/launchers.cpp). */
+#ifndef PK_GEMM_ARGS_H
+#define PK_GEMM_ARGS_H
+
+#include <stdint.h>
+
+typedef struct pk_gemm_args {
+  const uint16_t *A;         /* bf16 [M, K] */
+  const uint16_t *B;         /* bf16 [K, N] */
+  uint16_t *C;               /* bf16 [M, N] */
+  const uint16_t *bias;      /* bf16 [N] (epilogues 1 and 2) */
+  const uint16_t *R;         /* bf16 [M, N] residual (epilogues 2 and 3) */
+  const uint16_t *gelu_tab;  /* device GELU table (epilogue 1) */
+  int M, N, K;
+} pk_gemm_args;
+
+#endif /* PK_GEMM_ARGS_H */

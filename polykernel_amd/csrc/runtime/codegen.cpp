@@ -11,9 +11,15 @@
 // changes on disk is refused (CodeObject::Load) and dropped
 // (KernelCache::InvalidateStale).
 //
-// Emitted entry points (matmul_int8, matmul_int8_gelu, matmul_int8_residual):
-//   pk_int8_stream(pk_i8s_args)   grid (slices * splits, m-blocks), 64 * num_warps threads
-//   pk_int8_reduce(pk_i8s_args)   the split reduction, 256 threads
+// Emitted entry points:
+//   matmul_int8, matmul_int8_gelu, matmul_int8_residual (int8_stream.hpp):
+//     pk_int8_stream(pk_i8s_args)  grid (slices * splits, m-blocks), 64 * num_warps threads
+//     pk_int8_reduce(pk_i8s_args)  the split reduction, 256 threads
+//   matmul, fused_matmul_bias_gelu, fused_matmul_bias_residual (gemm_kernels.hpp):
+//     pk_gemm(pk_gemm_args)        grid ceil(M/block_m) * ceil(N/block_n), 64 * num_warps threads;
+//                                  block_k 32: the DMA-ring kernel at shared_memory_stages,
+//                                  block_k 64: the register-staged kernel (vector_width 8:
+//                                  16-byte loads, 1: element loads)
 #include <fcntl.h>
 #include <spawn.h>
 #include <sys/wait.h>
@@ -42,6 +48,35 @@ int Int8Epilogue(const std::string &op) {
   if (op == "matmul_int8_gelu") return 1;
   if (op == "matmul_int8_residual") return 2;
   return -1;
+}
+
+// Epilogue of a GEMM-family op (gemm_kernels.hpp Epi); the residual op's
+// object serves calls without a bias too (the kernels read a null bias as 0).
+int GemmEpilogue(const std::string &op) {
+  if (op == "matmul") return 0;
+  if (op == "fused_matmul_bias_gelu") return 1;
+  if (op == "fused_matmul_bias_residual") return 2;
+  return -1;
+}
+
+// The kernel template a GEMM config instantiates (the variants of
+// gemm.hip gemm_variant_config): returns false for a config it does not know.
+bool GemmInstance(const Config &c, int epi, std::string &body, int &threads) {
+  threads = 64 * c.num_warps;
+  if (c.block_k == 32 && c.block_m == 256 && c.block_n == 256 && c.num_warps == 8 &&
+      (c.shared_memory_stages == 4 || c.shared_memory_stages == 5)) {
+    body = "pk::gk::gemm_dma_body<" + std::to_string(epi) + ", " + std::to_string(c.shared_memory_stages) + ", 8, 4>";
+    return true;
+  }
+  if (c.block_k != 64 || (c.vector_width != 8 && c.vector_width != 1)) return false;
+  int wm = 0, wn = 0;
+  if (c.block_m == 256 && c.block_n == 256 && c.num_warps == 8) wm = 2, wn = 4;
+  else if ((c.block_m == 128 || c.block_m == 64) && c.block_n == c.block_m && c.num_warps == 4) wm = 2, wn = 2;
+  else return false;
+  body = "pk::gk::gemm_reg_body<" + std::to_string(c.block_m) + ", " + std::to_string(c.block_n) + ", " +
+         std::to_string(wm) + ", " + std::to_string(wn) + ", " + std::to_string(epi) + ", " +
+         (c.vector_width == 8 ? "true" : "false") + ">";
+  return true;
 }
 
 std::string Hipcc() {
@@ -82,9 +117,10 @@ bool RunChild(const std::vector<std::string> &argv, const std::string &log, std:
 }  // namespace
 
 bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
-  const int epi = Int8Epilogue(e.op);
-  if (epi < 0) {
-    error = "the emitter instantiates the int8 ops (matmul_int8, matmul_int8_gelu, matmul_int8_residual); " +
+  const int epi = Int8Epilogue(e.op), gepi = GemmEpilogue(e.op);
+  if (epi < 0 && gepi < 0) {
+    error = "the emitter instantiates the GEMM and int8 ops (matmul, fused_matmul_bias_gelu, "
+            "fused_matmul_bias_residual, matmul_int8, matmul_int8_gelu, matmul_int8_residual); " +
             e.op + " is served by the linked kernels";
     return false;
   }
@@ -99,6 +135,23 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
     return false;
   }
   const Config &c = e.best;
+  if (gepi >= 0) {
+    std::string body;
+    int threads = 0;
+    if (!GemmInstance(c, gepi, body, threads)) {
+      error = "config {" + autotune::ToString(c) + "} has no GEMM kernel template";
+      return false;
+    }
+    std::ostringstream s;
+    s << "// Emitted by the polykernel_amd gfx950 emitter for " << runtime::FormatKey(e.gpu, e.op, e.shape) << "\n"
+      << "// config: " << autotune::ToString(c) << "\n"
+      << "#include \"gemm_kernels.hpp\"\n\n"
+      << "extern \"C\" __global__ __launch_bounds__(" << threads << (c.block_k == 32 ? ", 1" : "")
+      << ") void pk_gemm(pk_gemm_args g) {\n"
+      << "  " << body << "(g);\n}\n";
+    source = s.str();
+    return true;
+  }
   const int nt = c.block_n / (16 * c.num_warps), mt = c.block_m / 16;
   std::ostringstream s;
   s << "// Emitted by the polykernel_amd gfx950 emitter for " << runtime::FormatKey(e.gpu, e.op, e.shape) << "\n"
@@ -159,7 +212,7 @@ bool EmitCodeObject(runtime::KernelCache &cache, const CacheEntry &e, const std:
   const Config &c = e.best;
   std::ostringstream name;
   name << e.op << "_M" << e.shape.m << "_N" << e.shape.n << "_K" << e.shape.k << "_" << c.block_m << "x" << c.block_n
-       << "x" << c.block_k << "_w" << c.num_warps << "_s" << c.shared_memory_stages;
+       << "x" << c.block_k << "_w" << c.num_warps << "_s" << c.shared_memory_stages << "_v" << c.vector_width;
   const std::string base = std::filesystem::absolute(std::filesystem::path(out_dir) / name.str()).string();
   {
     std::ofstream out(base + ".hip");

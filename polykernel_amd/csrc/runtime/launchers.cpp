@@ -10,11 +10,13 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <mutex>
 
 #include "../../../include/polykernel_amd_runtime.hpp"
+#include "../gemm_args.h"
 #include "../int8_args.h"
 #include "../workspace.hpp"
 
@@ -80,8 +82,7 @@ LaunchFn Int8Launcher(int epi) {
 struct ModuleTable {
   struct Loaded {
     CodeObject module;
-    void *stream_fn = nullptr;
-    void *reduce_fn = nullptr;
+    std::vector<void *> fns;  // the entry points asked for, in order
   };
   const KernelCache &cache;
   std::mutex mu;
@@ -89,15 +90,20 @@ struct ModuleTable {
 
   explicit ModuleTable(const KernelCache &c) : cache(c) {}
 
-  Loaded *Get(const CachedBinary &bin, std::string &error) {
+  // The module of `bin` with the entry points `names` resolved (an object
+  // serves one op, so the names are the same on every call for a binary).
+  Loaded *Get(const CachedBinary &bin, std::initializer_list<const char *> names, std::string &error) {
     std::lock_guard<std::mutex> lock(mu);
     const std::string key = bin.so_path + "#" + bin.kernel_hash;
     auto it = loaded.find(key);
     if (it != loaded.end()) return it->second.get();
     auto l = std::make_unique<Loaded>();
     if (!l->module.Load(bin, error)) return nullptr;
-    if (!(l->stream_fn = l->module.Function("pk_int8_stream", error))) return nullptr;
-    if (!(l->reduce_fn = l->module.Function("pk_int8_reduce", error))) return nullptr;
+    for (const char *n : names) {
+      void *f = l->module.Function(n, error);
+      if (!f) return nullptr;
+      l->fns.push_back(f);
+    }
     Loaded *raw = l.get();
     loaded.emplace(key, std::move(l));
     return raw;
@@ -106,8 +112,9 @@ struct ModuleTable {
 
 bool Aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-bool ModuleLaunch(void *fn, unsigned gx, unsigned gy, unsigned threads, void *stream, pk_i8s_args &args,
-                  const char *what, std::string &error) {
+template <typename Args>
+bool ModuleLaunch(void *fn, unsigned gx, unsigned gy, unsigned threads, void *stream, Args &args, const char *what,
+                  std::string &error) {
   void *params[] = {&args};
   const hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), gx, gy, 1, threads, 1, 1, 0,
                                              static_cast<hipStream_t>(stream), params, nullptr);
@@ -139,7 +146,7 @@ LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
               "; emit one (python -m polykernel_amd.emit)";
       return false;
     }
-    ModuleTable::Loaded *mod = table->Get(*bin, error);
+    ModuleTable::Loaded *mod = table->Get(*bin, {"pk_int8_stream", "pk_int8_reduce"}, error);
     if (!mod) return false;
     if (!Aligned16(p->A) || !Aligned16(p->Wq) || !Aligned16(p->scale) || !Aligned16(p->C) ||
         (epi == 2 && !Aligned16(p->residual))) {
@@ -176,15 +183,62 @@ LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
     }
     pk_i8s_args a{p->A, p->Wq, p->scale, static_cast<float *>(ws), p->C, epi == 2 ? p->residual : nullptr, tab,
                   p->M, p->N, p->K, splits, split_steps, slices * splits};
-    if (!ModuleLaunch(mod->stream_fn, (unsigned)(slices * splits), (unsigned)mblocks, 64u * c.num_warps, p->stream, a,
+    if (!ModuleLaunch(mod->fns[0], (unsigned)(slices * splits), (unsigned)mblocks, 64u * c.num_warps, p->stream, a,
                       "pk_int8_stream", error))
       return false;
     if (splits > 1) {
       const long long groups = (long long)p->M * p->N / 8;
       const unsigned blocks = (unsigned)std::min<long long>((groups + 255) / 256, 4096);
-      if (!ModuleLaunch(mod->reduce_fn, blocks, 1, 256, p->stream, a, "pk_int8_reduce", error)) return false;
+      if (!ModuleLaunch(mod->fns[1], blocks, 1, 256, p->stream, a, "pk_int8_reduce", error)) return false;
     }
     return true;
+  };
+}
+
+// GEMM-family code objects (pk_gemm): the launch geometry follows from the
+// config -- block_m x block_n tiles, 64 * num_warps threads -- and the
+// operand checks are the linked path's for the same config (gemm.hip
+// gemm_run_config): the DMA-ring kernel (block_k 32) and 16-byte loads
+// (vector_width 8) need 16-byte aligned operands, the DMA kernel also an
+// aligned C, residual and bias.
+LaunchFn CodeObjectGemmLauncher(int epi, std::shared_ptr<ModuleTable> table) {
+  return [epi, table](const CacheEntry &e, void *io, std::string &error) {
+    MatmulIO *p = Cast<MatmulIO>(io, error);
+    if (!p) return false;
+    const uint16_t *R = epi == 2 ? p->residual : nullptr;
+    if (!p->A || !p->B || !p->C || (epi == 1 && !p->bias) || (epi == 2 && !R)) {
+      error = std::string(e.op) + " code object: null tensor pointer";
+      return false;
+    }
+    if (!CheckEntry(e, p->M, p->N, p->K, error)) return false;
+    const Config &c = e.best;
+    const bool dma = c.block_k == 32;
+    const bool vec = dma || c.vector_width == 8;
+    if (vec && !(Aligned16(p->A) && Aligned16(p->B))) {
+      error = "code-object GEMM config {" + autotune::ToString(c) + "} needs 16-byte aligned A and B";
+      return false;
+    }
+    const uint16_t *bias = epi == 0 ? nullptr : p->bias;
+    if (dma && !(Aligned16(p->C) && (!R || Aligned16(R)) && (!bias || Aligned16(bias)))) {
+      error = "code-object GEMM config {" + autotune::ToString(c) + "} needs 16-byte aligned C, residual and bias";
+      return false;
+    }
+    const std::optional<CachedBinary> bin = table->cache.GetBinary(e.gpu, e.op, e.shape);
+    if (!bin) {
+      error = "no code object cached for " + FormatKey(e.gpu, e.op, e.shape) +
+              "; emit one (python -m polykernel_amd.emit)";
+      return false;
+    }
+    ModuleTable::Loaded *mod = table->Get(*bin, {"pk_gemm"}, error);
+    if (!mod) return false;
+    const uint16_t *tab = nullptr;
+    if (epi == 1 && pk_gelu_table(&tab) != PK_OK) {
+      error = std::string("GELU table: ") + pk_last_error();
+      return false;
+    }
+    pk_gemm_args a{p->A, p->B, p->C, bias, R, tab, p->M, p->N, p->K};
+    const unsigned tiles = (unsigned)(((p->M + c.block_m - 1) / c.block_m) * ((p->N + c.block_n - 1) / c.block_n));
+    return ModuleLaunch(mod->fns[0], tiles, 1, 64u * c.num_warps, p->stream, a, "pk_gemm", error);
   };
 }
 
@@ -192,6 +246,9 @@ LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
 
 void RegisterCodeObjectLaunchers(Runtime &rt, const KernelCache &cache) {
   auto table = std::make_shared<ModuleTable>(cache);
+  rt.RegisterLauncher("matmul", CodeObjectGemmLauncher(0, table));
+  rt.RegisterLauncher("fused_matmul_bias_gelu", CodeObjectGemmLauncher(1, table));
+  rt.RegisterLauncher("fused_matmul_bias_residual", CodeObjectGemmLauncher(2, table));
   rt.RegisterLauncher("matmul_int8", CodeObjectInt8Launcher(0, table));
   rt.RegisterLauncher("matmul_int8_gelu", CodeObjectInt8Launcher(1, table));
   rt.RegisterLauncher("matmul_int8_residual", CodeObjectInt8Launcher(2, table));

@@ -1,11 +1,12 @@
-"""Emit the gfx950 code objects of a tuning cache's int8 entries.
+"""Emit the gfx950 code objects of a tuning cache's GEMM-family and int8 entries.
 
     python -m polykernel_amd.emit                      # committed cache -> polykernel_amd/tuning/gfx950.d
     python -m polykernel_amd.emit --cache X.json --out DIR
 
-For every int8 entry of the cache the emitter (csrc/runtime/codegen.cpp)
-writes a HIP source that instantiates the streaming kernel at the entry's
-configuration, compiles it for gfx950 with hipcc --genco (no GPU needed) and
+For every GEMM-family and int8 entry of the cache the emitter
+(csrc/runtime/codegen.cpp) writes a HIP source that instantiates the kernel
+template (gemm_kernels.hpp, int8_stream.hpp) at the entry's configuration,
+compiles it for gfx950 with hipcc --genco (no GPU needed) and
 records the code object's path and FNV-1a hash beside the entry.  The result
 is persisted as DIR/tuning_db.json + DIR/binaries.json (the KernelCache
 persistence format); runtime.Runtime(..., code_objects=True) over
@@ -22,15 +23,63 @@ from pathlib import Path
 from . import runtime as rt
 
 DEFAULT_OUT = rt.TUNING_FILE.with_suffix(".d")
-INT8_OPS = ("matmul_int8", "matmul_int8_gelu", "matmul_int8_residual")
+EMIT_OPS = ("matmul", "fused_matmul_bias_gelu", "fused_matmul_bias_residual",
+            "matmul_int8", "matmul_int8_gelu", "matmul_int8_residual")
 
 
 def emit(cache_file: Path = rt.TUNING_FILE, out_dir: Path = DEFAULT_OUT, verbose: bool = True) -> int:
-    """Emit every int8 entry of cache_file into out_dir; returns the count."""
+    """Emit every GEMM-family and int8 entry of cache_file into out_dir; returns the count."""
     doc = json.loads(Path(cache_file).read_text())
-    entries = [e for e in doc["entries"] if e["op"] in INT8_OPS and e["validated"]]
+    entries = [e for e in doc["entries"] if e["op"] in EMIT_OPS and e["validated"]]
     cache = rt.KernelCache()
     cache.load_tuning_cache(Path(cache_file).read_text())
+    return _emit_entries(entries, cache, Path(out_dir), verbose)
+
+
+# Conformance set: every kernel template the emitter instantiates, at small
+# shapes, so that the GPU tests can compare each emitted object with the
+# linked kernel at the same configuration.  These entries are not tuned
+# (scored_by "model", no time); they live in their own cache directory and
+# are never served by the default runtimes.
+CONFORMANCE_OUT = rt.TUNING_FILE.with_name("gfx950.conformance.d")
+GEMM_SHAPE = (200, 264, 256)  # ragged M and N tiles for every tile size
+INT8_SHAPE = (24, 1040, 1024)
+
+
+def conformance_entries() -> list:
+    out = []
+
+    def entry(op, shape, dtype, cfg):
+        M, N, K = shape
+        return {"gpu": "gfx950", "op": op, "shape": {"M": M, "N": N, "K": K, "dtype": dtype}, "best": cfg,
+                "scored_by": "model", "time_ms": None, "validated": True,
+                "correctness": {"cosine": 1.0, "max_rel_err": 0.0, "pcc": 1.0}}
+
+    for op in ("matmul", "fused_matmul_bias_gelu", "fused_matmul_bias_residual"):
+        for cfg in rt.candidates(op, *GEMM_SHAPE):
+            out.append(entry(op, GEMM_SHAPE, "bf16", cfg))
+    cands = rt.candidates("matmul_int8_residual", *INT8_SHAPE)
+    split = next(c for c in cands if c["block_k"] < INT8_SHAPE[2])
+    for op in ("matmul_int8", "matmul_int8_gelu", "matmul_int8_residual"):
+        out.append(entry(op, INT8_SHAPE, "int8", cands[0]))
+        out.append(entry(op, INT8_SHAPE, "int8", split))
+    return out
+
+
+def emit_conformance(out_dir: Path = CONFORMANCE_OUT, verbose: bool = False) -> int:
+    """Emit the conformance set into out_dir/objects and list every (entry,
+    code object, hash) in out_dir/manifest.json (a cache holds one entry per
+    (op, shape), so the GPU test builds one cache per manifest line)."""
+    done = _emit_entries(conformance_entries(), None, Path(out_dir), verbose)
+    manifest = [{"entry": e, "so_path": b["so_path"], "kernel_hash": b["kernel_hash"]} for e, b in done]
+    (Path(out_dir) / "manifest.json").write_text(json.dumps(manifest, indent=1) + "\n")
+    return len(done)
+
+
+def _emit_entries(entries, cache, out_dir: Path, verbose: bool):
+    """Emit each entry's code object; with a cache, record the objects in it
+    and persist it to out_dir (returns the count), else return the list of
+    (entry, binary) pairs."""
     objects = Path(out_dir) / "objects"
 
     # compile in parallel (each a hipcc child process), record in order
@@ -40,6 +89,8 @@ def emit(cache_file: Path = rt.TUNING_FILE, out_dir: Path = DEFAULT_OUT, verbose
 
     with ThreadPoolExecutor(max_workers=max(1, min(8, len(entries)))) as ex:
         done = list(ex.map(one, entries))
+    if cache is None:
+        return done
     for e, binary in done:
         sh = e["shape"]
         cache.put_binary(e["gpu"], e["op"], sh["M"], sh["N"], sh["K"], sh["dtype"], binary["so_path"],

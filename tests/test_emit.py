@@ -9,7 +9,7 @@ import shutil
 
 import pytest
 
-from polykernel_amd import _lib
+from polykernel_amd import _lib, emit
 from polykernel_amd import runtime as rt
 
 
@@ -30,11 +30,39 @@ def test_emit_source_instantiates_the_config():
     assert "gfx950/matmul_int8_gelu/M=16,N=1024,K=2048,int8" in src
 
 
+def gemm_entry(op="fused_matmul_bias_gelu", M=4096, N=16384, K=4096, config=None):
+    cfg = config or rt.default_config(op, M, N, K)
+    return {"gpu": "gfx950", "op": op, "shape": {"M": M, "N": N, "K": K, "dtype": "bf16"}, "best": cfg,
+            "scored_by": "measure", "time_ms": 0.45, "validated": True,
+            "correctness": {"cosine": 1.0, "max_rel_err": 0.0, "pcc": 1.0}}
+
+
+def test_emit_source_gemm_templates():
+    """Each GEMM config names the template it instantiates: the DMA ring
+    (block_k 32) at its depth, the register-staged kernels at their tile and
+    vector width."""
+    src = rt.emit_source(gemm_entry())
+    assert "#include \"gemm_kernels.hpp\"" in src
+    assert "__launch_bounds__(512, 1) void pk_gemm(pk_gemm_args g)" in src
+    assert "pk::gk::gemm_dma_body<1, 5, 8, 4>(g);" in src
+    shape = (200, 264, 256)
+    for cfg in rt.candidates("fused_matmul_bias_residual", *shape):
+        src = rt.emit_source(gemm_entry("fused_matmul_bias_residual", *shape, config=cfg))
+        if cfg["block_k"] == 32:
+            assert f"gemm_dma_body<2, {cfg['shared_memory_stages']}, 8, 4>" in src
+        else:
+            wm, wn = (2, 4) if cfg["block_m"] == 256 else (2, 2)
+            aligned = "true" if cfg["vector_width"] == 8 else "false"
+            assert (f"gemm_reg_body<{cfg['block_m']}, {cfg['block_n']}, {wm}, {wn}, 2, {aligned}>" in src), src
+            assert f"__launch_bounds__({64 * cfg['num_warps']}) void pk_gemm" in src
+
+
 def test_emit_refuses_other_ops_and_foreign_configs():
-    gemm = int8_entry()
-    gemm.update(op="matmul", shape={"M": 256, "N": 256, "K": 256, "dtype": "bf16"})
+    rows = int8_entry()
+    rows.update(op="fused_residual_rmsnorm", shape={"M": 64, "N": 4096, "K": 0, "dtype": "bf16"},
+                best=rt.default_config("fused_residual_rmsnorm", 64, 4096, 0))
     with pytest.raises(rt.RuntimeError_) as ei:
-        rt.emit_source(gemm)
+        rt.emit_source(rows)
     assert "served by the linked kernels" in ei.value.message
     bad = int8_entry()
     bad["best"]["block_n"] = 96
@@ -93,5 +121,42 @@ def test_built_code_object_cache_matches_committed_tuning():
     for e in doc["entries"]:
         sh = e["shape"]
         b = cache.get_binary(e["gpu"], e["op"], sh["M"], sh["N"], sh["K"], sh["dtype"])
-        assert (b is not None) == e["op"].startswith("matmul_int8"), e["op"]
+        assert (b is not None) == (e["op"] in emit.EMIT_OPS), e["op"]
         assert cache.select(e["gpu"], e["op"], sh["M"], sh["N"], sh["K"], sh["dtype"])["best"] == e["best"]
+
+
+def test_conformance_objects_built():
+    """build() emitted every GEMM template (each epilogue) and int8 variant of
+    the conformance set; each manifest line names an ELF whose hash matches."""
+    m = emit.CONFORMANCE_OUT / "manifest.json"
+    if not m.exists():
+        pytest.skip("conformance objects not built (run __graft_entry__.build())")
+    lines = json.loads(m.read_text())
+    assert len(lines) == len(emit.conformance_entries())
+    assert len({l["so_path"] for l in lines}) == len(lines)  # one object per (op, config)
+    for l in lines:
+        data = open(l["so_path"], "rb").read(4)
+        assert data == b"\x7fELF"
+        assert rt.hash_file(l["so_path"]) == l["kernel_hash"]
+
+
+def test_code_object_gemm_launcher_checks_before_any_device_call():
+    """Null operands, a shape other than the entry's and misaligned operands
+    for a 16-byte config are refused without touching the device."""
+    cache = rt.KernelCache()
+    e = gemm_entry()
+    cache.put(e)
+    r = rt.Runtime(cache, fixed_arch="gfx950", code_objects=True)
+    io = rt.MatmulIO(A=256, B=256, C=256, bias=None, residual=None, M=4096, N=16384, K=4096)
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_matmul_bias_gelu", 4096, 16384, 4096, io)
+    assert "null tensor pointer" in ei.value.message
+    io.bias = 256
+    io.A = 258  # not 16-byte aligned
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_matmul_bias_gelu", 4096, 16384, 4096, io)
+    assert "16-byte aligned" in ei.value.message
+    io.A = 256
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_matmul_bias_gelu", 4096, 16384, 4096, io)
+    assert "no code object cached" in ei.value.message

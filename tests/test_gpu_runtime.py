@@ -512,3 +512,91 @@ def test_code_objects_serve_config5_bit_identical(gpu, op, M, N, Kd, epi):
     # and a second launch (module already loaded) is identical too
     served.run(op, M, N, Kd, io)
     assert np.array_equal(from_dev(out), direct)
+
+
+@pytest.mark.parametrize("op,M,N,Kd,epi", [("fused_matmul_bias_gelu", 4096, 16384, 4096, 1),
+                                            ("fused_matmul_bias_residual", 4096, 4096, 16384, 2)])
+def test_code_objects_serve_config2_gemms_bit_identical(gpu, op, M, N, Kd, epi):
+    """The committed config-2 GEMM entries served from their emitted code
+    objects (hipModuleLoad + hipModuleLaunchKernel) give the bits of the
+    linked kernel at the same configuration, on the first and a later launch."""
+    import torch
+
+    from polykernel_amd import kernels
+
+    assert rt.CODE_OBJECT_DIR.exists(), "code objects missing: run __graft_entry__.build()"
+    cache = rt.code_object_cache()
+    served = rt.Runtime(cache, code_objects=True)
+    entry = served.resolve(op, M, N, Kd)
+    assert cache.get_binary("gfx950", op, M, N, Kd, "bf16") is not None
+    _say(f"code object {op} {entry['best']}")
+    a = to_dev(synth.normal_bf16((M, Kd), 101))
+    b = to_dev(synth.normal_bf16((Kd, N), 102, 1.0 / math.sqrt(Kd)))
+    bias = to_dev(synth.normal_bf16((N,), 103, 0.02))
+    r = to_dev(synth.normal_bf16((M, N), 104)) if epi == 2 else None
+    out = _empty_bf16((M, N))
+    io = rt.MatmulIO(A=_ptr(a), B=_ptr(b), C=_ptr(out), bias=_ptr(bias), residual=_ptr(r), M=M, N=N, K=Kd,
+                     stream=_stream())
+    served.run(op, M, N, Kd, io)
+    direct = _empty_bf16((M, N))
+    _lib.check(_lib.load().pk_gemm_config_ex(epi, _ptr(a), _ptr(b), _ptr(direct), _ptr(bias), _ptr(r), M, N, Kd,
+                                             C.byref(_cfg(entry["best"])), _stream()), "pk_gemm_config_ex")
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), direct.view(torch.int16))
+    out.zero_()
+    served.run(op, M, N, Kd, io)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), direct.view(torch.int16))
+
+
+def test_conformance_code_objects_bit_identical(gpu):
+    """Every kernel template the emitter instantiates (the GEMM family's DMA
+    ring at both depths and the register-staged tiles at both vector widths,
+    with every epilogue; int8 with and without a K split), served from its
+    code object, equals the linked kernel at the same configuration bit for
+    bit (ragged M and N tiles; null bias for the residual op included)."""
+    import torch
+
+    from polykernel_amd import emit
+
+    m = emit.CONFORMANCE_OUT / "manifest.json"
+    assert m.exists(), "conformance objects missing: run __graft_entry__.build()"
+    lines = json.loads(m.read_text())
+    lib = _lib.load()
+    for i, line in enumerate(lines):
+        e = line["entry"]
+        op, sh, cfg = e["op"], e["shape"], e["best"]
+        M, N, Kd = sh["M"], sh["N"], sh["K"]
+        _say(f"conformance {op} {M}x{N}x{Kd} {cfg}")
+        cache = rt.KernelCache()
+        cache.put(e)
+        cache.put_binary("gfx950", op, M, N, Kd, sh["dtype"], line["so_path"], line["kernel_hash"])
+        served = rt.Runtime(cache, code_objects=True)
+        out, direct = _empty_bf16((M, N)), _empty_bf16((M, N))
+        a = to_dev(synth.normal_bf16((M, Kd), 110 + i))
+        r = to_dev(synth.normal_bf16((M, N), 111 + i))
+        if sh["dtype"] == "bf16":
+            epi = {"matmul": 0, "fused_matmul_bias_gelu": 1, "fused_matmul_bias_residual": 2}[op]
+            b = to_dev(synth.normal_bf16((Kd, N), 112 + i, 1.0 / math.sqrt(Kd)))
+            for bias in ([to_dev(synth.normal_bf16((N,), 113 + i, 0.02))] +
+                         ([None] if epi == 2 else [])):
+                rr = r if epi == 2 else None
+                io = rt.MatmulIO(A=_ptr(a), B=_ptr(b), C=_ptr(out), bias=_ptr(bias), residual=_ptr(rr), M=M, N=N,
+                                 K=Kd, stream=_stream())
+                served.run(op, M, N, Kd, io)
+                _lib.check(lib.pk_gemm_config_ex(epi, _ptr(a), _ptr(b), _ptr(direct), _ptr(bias), _ptr(rr), M, N,
+                                                 Kd, C.byref(_cfg(cfg)), _stream()), "pk_gemm_config_ex")
+                torch.cuda.synchronize()
+                assert torch.equal(out.view(torch.int16), direct.view(torch.int16)), (op, cfg, bias is None)
+        else:
+            from polykernel_amd import kernels
+
+            epi = {"matmul_int8": 0, "matmul_int8_gelu": 1, "matmul_int8_residual": 2}[op]
+            wq, s = kernels.quantize_per_channel(to_dev(synth.normal_bf16((Kd, N), 114 + i, 1.0 / math.sqrt(Kd))))
+            rr = r if epi == 2 else None
+            io = rt.MatmulInt8IO(A=_ptr(a), Wq=_ptr(wq), scale=_ptr(s), C=_ptr(out), residual=_ptr(rr), M=M, N=N,
+                                 K=Kd, workspace=None, workspace_bytes=0, stream=_stream())
+            served.run(op, M, N, Kd, io)
+            direct = kernels.matmul_int8_ex(epi, a, wq, s, residual=rr, config=cfg)
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), direct.view(torch.int16)), (op, cfg)
