@@ -378,24 +378,6 @@ __global__ __launch_bounds__(kBlock) void kv_concat_kernel(const uint16_t *__res
   }
 }
 
-// In-place append: rows [S_cache, S_cache + S_new) of a cache with capacity Cap.
-__global__ __launch_bounds__(kBlock) void kv_append_inplace_kernel(uint16_t *__restrict__ cache,
-                                                                   const uint16_t *__restrict__ neu,
-                                                                   int64_t BH, int64_t Sc,
-                                                                   int64_t Sn, int64_t D,
-                                                                   int64_t Cap, int vec) {
-  const int64_t per = vec ? D / 8 : D;
-  const int64_t total = BH * Sn * per;
-  const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
-    const int64_t u = t % per, rs = t / per, s = rs % Sn, bh = rs / Sn;
-    const uint16_t *src = neu + (bh * Sn + s) * D;
-    uint16_t *dst = cache + (bh * Cap + Sc + s) * D;
-    if (vec) st16(dst + u * 8, ld16(src + u * 8));
-    else dst[u] = src[u];
-  }
-}
-
 // ---------------------------------------------------------------------------
 // int8 per-output-channel quantisation (tests/golden/quant_golden.py:71-83).
 // Pass 1: amax[n] = max_k |W[k,n]| as float bits (non-negative floats order
@@ -464,16 +446,6 @@ int gelu_launch(const uint16_t *in, uint16_t *out, int64_t n, hipStream_t st) {
   if (aligned16(in) && aligned16(out)) gelu_kernel<<<grid_for(n, 8), kBlock, 0, st>>>(in, out, n, tab);
   else gelu_scalar_kernel<<<grid_for(n), kBlock, 0, st>>>(in, out, n, tab);
   PK_LAUNCH_CHECK("gelu");
-  return PK_OK;
-}
-
-int kv_append_inplace_launch(uint16_t *cache, const uint16_t *neu, int64_t BH, int64_t Sc,
-                             int64_t Sn, int64_t D, int64_t cap, hipStream_t st) {
-  if (BH * Sn * D == 0) return PK_OK;
-  const int vec = (D % 8 == 0) && aligned16(cache) && aligned16(neu);
-  const int64_t units = BH * Sn * (vec ? D / 8 : D);
-  kv_append_inplace_kernel<<<grid_for(units), kBlock, 0, st>>>(cache, neu, BH, Sc, Sn, D, cap, vec);
-  PK_LAUNCH_CHECK("kv_append_inplace");
   return PK_OK;
 }
 

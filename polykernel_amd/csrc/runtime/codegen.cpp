@@ -20,6 +20,15 @@
 //                                  block_k 32: the DMA-ring kernel at shared_memory_stages,
 //                                  block_k 64: the register-staged kernel (vector_width 8:
 //                                  16-byte loads, 1: element loads)
+//   fused_kv_append_attention (attention_kernels.hpp), the flash kernel's tile shapes (num_warps 8):
+//     pk_fa_fused(pk_fa_args)      the flash kernel with the in-place append, 512 threads
+//     pk_fa_combine(pk_fa_args)    the merge of key splits, 256 threads
+//   and the generic kernel (num_warps 4, block_k = padded head dim):
+//     pk_att / pk_att_unaligned(pk_att_args), pk_att_combine(pk_att_args),
+//     pk_kv_append(pk_kv_append_args)
+//   The runtime hands these to the library's attention dispatcher
+//   (attention_module.hpp), which makes the linked path's tile-shape, key-split
+//   and workspace decisions and launches the object's entry points.
 #include <fcntl.h>
 #include <spawn.h>
 #include <sys/wait.h>
@@ -118,9 +127,11 @@ bool RunChild(const std::vector<std::string> &argv, const std::string &log, std:
 
 bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
   const int epi = Int8Epilogue(e.op), gepi = GemmEpilogue(e.op);
-  if (epi < 0 && gepi < 0) {
-    error = "the emitter instantiates the GEMM and int8 ops (matmul, fused_matmul_bias_gelu, "
-            "fused_matmul_bias_residual, matmul_int8, matmul_int8_gelu, matmul_int8_residual); " +
+  const bool attention = e.op == "fused_kv_append_attention";
+  if (epi < 0 && gepi < 0 && !attention) {
+    error = "the emitter instantiates the GEMM, int8 and attention ops (matmul, fused_matmul_bias_gelu, "
+            "fused_matmul_bias_residual, matmul_int8, matmul_int8_gelu, matmul_int8_residual, "
+            "fused_kv_append_attention); " +
             e.op + " is served by the linked kernels";
     return false;
   }
@@ -135,6 +146,31 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
     return false;
   }
   const Config &c = e.best;
+  if (attention) {
+    const int dp = c.block_k;
+    std::ostringstream s;
+    s << "// Emitted by the polykernel_amd gfx950 emitter for " << runtime::FormatKey(e.gpu, e.op, e.shape) << "\n"
+      << "// config: " << autotune::ToString(c) << "\n"
+      << "#include \"attention_kernels.hpp\"\n\n";
+    if (c.num_warps == 8) {  // the flash kernel at this tile shape
+      const int qg = c.block_m / 32;
+      s << "extern \"C\" __global__ __launch_bounds__(512, 1) void pk_fa_fused(pk_fa_args g) {\n"
+        << "  pk::att::fa_body<" << dp << ", " << qg << ", true>(g);\n}\n\n"
+        << "extern \"C\" __global__ __launch_bounds__(256) void pk_fa_combine(pk_fa_args g) {\n"
+        << "  pk::att::fa_combine_body<" << dp << ">(g);\n}\n";
+    } else {
+      s << "extern \"C\" __global__ __launch_bounds__(256) void pk_att(pk_att_args g) {\n"
+        << "  pk::att::att_body<" << dp << ", true>(g);\n}\n\n"
+        << "extern \"C\" __global__ __launch_bounds__(256) void pk_att_unaligned(pk_att_args g) {\n"
+        << "  pk::att::att_body<" << dp << ", false>(g);\n}\n\n"
+        << "extern \"C\" __global__ __launch_bounds__(256) void pk_att_combine(pk_att_args g) {\n"
+        << "  pk::att::att_combine_body<" << dp << ">(g);\n}\n\n"
+        << "extern \"C\" __global__ __launch_bounds__(256) void pk_kv_append(pk_kv_append_args a) {\n"
+        << "  pk::att::kv_append_body(a);\n}\n";
+    }
+    source = s.str();
+    return true;
+  }
   if (gepi >= 0) {
     std::string body;
     int threads = 0;

@@ -16,6 +16,7 @@
 #include <mutex>
 
 #include "../../../include/polykernel_amd_runtime.hpp"
+#include "../attention_module.hpp"
 #include "../gemm_args.h"
 #include "../int8_args.h"
 #include "../workspace.hpp"
@@ -242,10 +243,52 @@ LaunchFn CodeObjectGemmLauncher(int epi, std::shared_ptr<ModuleTable> table) {
   };
 }
 
+// Attention code objects: the library's attention dispatcher makes the same
+// tile-shape, key-split, workspace and append decisions as for the linked
+// kernels and launches the object's entry points (attention_module.hpp).
+LaunchFn CodeObjectAttentionLauncher(std::shared_ptr<ModuleTable> table) {
+  return [table](const CacheEntry &e, void *io, std::string &error) {
+    KvAppendAttentionIO *p = Cast<KvAppendAttentionIO>(io, error);
+    if (!p) return false;
+    if (!p->Q || !p->Kc || !p->Vc || !p->O || (p->S_q > 0 && (!p->Kn || !p->Vn))) {
+      error = "fused_kv_append_attention code object: null tensor pointer";
+      return false;
+    }
+    if (!CheckEntry(e, p->S_q, (std::int64_t)p->S_cache + p->S_q, p->D, error)) return false;
+    const std::optional<CachedBinary> bin = table->cache.GetBinary(e.gpu, e.op, e.shape);
+    if (!bin) {
+      error = "no code object cached for " + FormatKey(e.gpu, e.op, e.shape) +
+              "; emit one (python -m polykernel_amd.emit)";
+      return false;
+    }
+    const bool flash = e.best.num_warps == 8;
+    ModuleTable::Loaded *m =
+        flash ? table->Get(*bin, {"pk_fa_fused", "pk_fa_combine"}, error)
+              : table->Get(*bin, {"pk_att", "pk_att_unaligned", "pk_att_combine", "pk_kv_append"}, error);
+    if (!m) return false;
+    AttModule mod;
+    if (flash) {
+      mod.fa_fused = m->fns[0];
+      mod.fa_combine = m->fns[1];
+    } else {
+      mod.att = m->fns[0];
+      mod.att_unaligned = m->fns[1];
+      mod.att_combine = m->fns[2];
+      mod.kv_append = m->fns[3];
+    }
+    const pk_config cfg = ToPk(e.best);
+    return Launched(fused_kv_append_attention_module(p->Q, p->Kc, p->Vc, p->Kn, p->Vn, p->O, p->B, p->H, p->S_q,
+                                                     p->S_cache, p->D, p->cache_capacity, p->scale, p->causal, &cfg,
+                                                     &mod, p->stream),
+                    e, error);
+  };
+}
+
 }  // namespace
 
 void RegisterCodeObjectLaunchers(Runtime &rt, const KernelCache &cache) {
   auto table = std::make_shared<ModuleTable>(cache);
+  rt.RegisterLauncher("fused_kv_append_attention", CodeObjectAttentionLauncher(table));
   rt.RegisterLauncher("matmul", CodeObjectGemmLauncher(0, table));
   rt.RegisterLauncher("fused_matmul_bias_gelu", CodeObjectGemmLauncher(1, table));
   rt.RegisterLauncher("fused_matmul_bias_residual", CodeObjectGemmLauncher(2, table));

@@ -1,11 +1,12 @@
-"""Emit the gfx950 code objects of a tuning cache's GEMM-family and int8 entries.
+"""Emit the gfx950 code objects of a tuning cache's GEMM-family, int8 and attention entries.
 
     python -m polykernel_amd.emit                      # committed cache -> polykernel_amd/tuning/gfx950.d
     python -m polykernel_amd.emit --cache X.json --out DIR
 
-For every GEMM-family and int8 entry of the cache the emitter
+For every GEMM-family, int8 and attention entry of the cache the emitter
 (csrc/runtime/codegen.cpp) writes a HIP source that instantiates the kernel
-template (gemm_kernels.hpp, int8_stream.hpp) at the entry's configuration,
+template (gemm_kernels.hpp, int8_stream.hpp, attention_kernels.hpp) at the
+entry's configuration,
 compiles it for gfx950 with hipcc --genco (no GPU needed) and
 records the code object's path and FNV-1a hash beside the entry.  The result
 is persisted as DIR/tuning_db.json + DIR/binaries.json (the KernelCache
@@ -24,11 +25,11 @@ from . import runtime as rt
 
 DEFAULT_OUT = rt.TUNING_FILE.with_suffix(".d")
 EMIT_OPS = ("matmul", "fused_matmul_bias_gelu", "fused_matmul_bias_residual",
-            "matmul_int8", "matmul_int8_gelu", "matmul_int8_residual")
+            "matmul_int8", "matmul_int8_gelu", "matmul_int8_residual", "fused_kv_append_attention")
 
 
 def emit(cache_file: Path = rt.TUNING_FILE, out_dir: Path = DEFAULT_OUT, verbose: bool = True) -> int:
-    """Emit every GEMM-family and int8 entry of cache_file into out_dir; returns the count."""
+    """Emit every GEMM-family, int8 and attention entry of cache_file into out_dir; returns the count."""
     doc = json.loads(Path(cache_file).read_text())
     entries = [e for e in doc["entries"] if e["op"] in EMIT_OPS and e["validated"]]
     cache = rt.KernelCache()
@@ -44,6 +45,7 @@ def emit(cache_file: Path = rt.TUNING_FILE, out_dir: Path = DEFAULT_OUT, verbose
 CONFORMANCE_OUT = rt.TUNING_FILE.with_name("gfx950.conformance.d")
 GEMM_SHAPE = (200, 264, 256)  # ragged M and N tiles for every tile size
 INT8_SHAPE = (24, 1040, 1024)
+ATT_SQ, ATT_SCACHE, ATT_HEAD_DIMS = 200, 256, (64, 128, 96, 256)
 
 
 def conformance_entries() -> list:
@@ -58,6 +60,12 @@ def conformance_entries() -> list:
     for op in ("matmul", "fused_matmul_bias_gelu", "fused_matmul_bias_residual"):
         for cfg in rt.candidates(op, *GEMM_SHAPE):
             out.append(entry(op, GEMM_SHAPE, "bf16", cfg))
+    # attention shape key (S_q, S_cache + S_q, D); S_cache 256 sits on the
+    # key step of both flash tile shapes, so the fused append applies
+    for D in ATT_HEAD_DIMS:
+        shape = (ATT_SQ, ATT_SCACHE + ATT_SQ, D)
+        for cfg in rt.candidates("fused_kv_append_attention", *shape):
+            out.append(entry("fused_kv_append_attention", shape, "bf16", cfg))
     cands = rt.candidates("matmul_int8_residual", *INT8_SHAPE)
     split = next(c for c in cands if c["block_k"] < INT8_SHAPE[2])
     for op in ("matmul_int8", "matmul_int8_gelu", "matmul_int8_residual"):

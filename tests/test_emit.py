@@ -160,3 +160,41 @@ def test_code_object_gemm_launcher_checks_before_any_device_call():
     with pytest.raises(rt.RuntimeError_) as ei:
         r.run("fused_matmul_bias_gelu", 4096, 16384, 4096, io)
     assert "no code object cached" in ei.value.message
+
+
+def att_entry(S_q=512, S_kv=4096, D=128, config=None):
+    cfg = config or rt.default_config("fused_kv_append_attention", S_q, S_kv, D)
+    return {"gpu": "gfx950", "op": "fused_kv_append_attention", "shape": {"M": S_q, "N": S_kv, "K": D, "dtype": "bf16"},
+            "best": cfg, "scored_by": "measure", "time_ms": 0.06, "validated": True,
+            "correctness": {"cosine": 1.0, "max_rel_err": 0.0, "pcc": 1.0}}
+
+
+def test_emit_source_attention_templates():
+    """Flash tile shapes instantiate the fused flash kernel and its merge; the
+    generic config the generic kernel (both alignments), its merge and the
+    in-place append."""
+    for cfg in rt.candidates("fused_kv_append_attention", 512, 4096, 128):
+        src = rt.emit_source(att_entry(config=cfg))
+        qg = cfg["block_m"] // 32
+        assert f"pk::att::fa_body<128, {qg}, true>(g);" in src
+        assert "void pk_fa_combine(pk_fa_args g)" in src and "pk::att::fa_combine_body<128>" in src
+    (gen,) = rt.candidates("fused_kv_append_attention", 100, 300, 200)
+    src = rt.emit_source(att_entry(100, 300, 200, gen))
+    for want in ("pk::att::att_body<256, true>(g);", "pk::att::att_body<256, false>(g);",
+                 "pk::att::att_combine_body<256>(g);", "pk::att::kv_append_body(a);"):
+        assert want in src
+
+
+def test_code_object_attention_launcher_checks_before_any_device_call():
+    cache = rt.KernelCache()
+    cache.put(att_entry())
+    r = rt.Runtime(cache, fixed_arch="gfx950", code_objects=True)
+    io = rt.KvAppendAttentionIO(Q=256, Kc=256, Vc=256, Kn=None, Vn=256, O=256, B=1, H=32, S_q=512, S_cache=3584,
+                                D=128, cache_capacity=4096, scale=0.088, causal=1)
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_kv_append_attention", 512, 4096, 128, io)
+    assert "null tensor pointer" in ei.value.message
+    io.Kn = 256
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_kv_append_attention", 512, 4096, 128, io)
+    assert "no code object cached" in ei.value.message

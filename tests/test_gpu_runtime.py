@@ -575,6 +575,9 @@ def test_conformance_code_objects_bit_identical(gpu):
         out, direct = _empty_bf16((M, N)), _empty_bf16((M, N))
         a = to_dev(synth.normal_bf16((M, Kd), 110 + i))
         r = to_dev(synth.normal_bf16((M, N), 111 + i))
+        if op == "fused_kv_append_attention":
+            _attention_served_equals_linked(served, e, seed=120 + i)
+            continue
         if sh["dtype"] == "bf16":
             epi = {"matmul": 0, "fused_matmul_bias_gelu": 1, "fused_matmul_bias_residual": 2}[op]
             b = to_dev(synth.normal_bf16((Kd, N), 112 + i, 1.0 / math.sqrt(Kd)))
@@ -600,3 +603,51 @@ def test_conformance_code_objects_bit_identical(gpu):
             direct = kernels.matmul_int8_ex(epi, a, wq, s, residual=rr, config=cfg)
             torch.cuda.synchronize()
             assert torch.equal(out.view(torch.int16), direct.view(torch.int16)), (op, cfg)
+
+
+def _attention_served_equals_linked(served, e, seed, B=1, H=4):
+    """One fused KV-append attention call through `served` (code objects)
+    and the same call through the linked kernels at the entry's config:
+    identical outputs and identical appended caches."""
+    import torch
+
+    lib = _lib.load()
+    Sq, Skv, D = e["shape"]["M"], e["shape"]["N"], e["shape"]["K"]
+    Sc = Skv - Sq
+    q = to_dev(synth.normal_bf16((B, H, Sq, D), seed))
+    kn, vn = to_dev(synth.normal_bf16((B, H, Sq, D), seed + 1)), to_dev(synth.normal_bf16((B, H, Sq, D), seed + 2))
+    kc0, vc0 = synth.normal_bf16((B, H, Sc, D), seed + 3), synth.normal_bf16((B, H, Sc, D), seed + 4)
+    scale = 1.0 / math.sqrt(D)
+    outs, caches = [], []
+    for use_module in (True, False):
+        kc = torch.zeros(B, H, Skv, D, dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros_like(kc)
+        kc[:, :, :Sc] = to_dev(kc0)
+        vc[:, :, :Sc] = to_dev(vc0)
+        o = _empty_bf16((B, H, Sq, D))
+        if use_module:
+            io = rt.KvAppendAttentionIO(Q=_ptr(q), Kc=_ptr(kc), Vc=_ptr(vc), Kn=_ptr(kn), Vn=_ptr(vn), O=_ptr(o),
+                                        B=B, H=H, S_q=Sq, S_cache=Sc, D=D, cache_capacity=Skv, scale=scale,
+                                        causal=1, stream=_stream())
+            served.run("fused_kv_append_attention", Sq, Skv, D, io)
+        else:
+            _lib.check(lib.pk_fused_kv_append_attention_config(
+                _ptr(q), _ptr(kc), _ptr(vc), _ptr(kn), _ptr(vn), _ptr(o), B, H, Sq, Sc, D, Skv, scale, 1,
+                C.byref(_cfg(e["best"])), _stream()), "attention config")
+        torch.cuda.synchronize()
+        outs.append(o.view(torch.int16).clone())
+        caches.append((kc.view(torch.int16).clone(), vc.view(torch.int16).clone()))
+    assert torch.equal(outs[0], outs[1]), (Sq, Skv, D, e["best"])
+    assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+
+
+def test_code_objects_serve_config3_attention_bit_identical(gpu):
+    """The committed config-3 attention entry (B1 H32 D128, 3584 + 512) served
+    from its emitted code object equals the linked kernels bit for bit."""
+    assert rt.CODE_OBJECT_DIR.exists(), "code objects missing: run __graft_entry__.build()"
+    cache = rt.code_object_cache()
+    served = rt.Runtime(cache, code_objects=True)
+    e = served.resolve("fused_kv_append_attention", 512, 4096, 128)
+    assert cache.get_binary("gfx950", "fused_kv_append_attention", 512, 4096, 128, "bf16") is not None
+    _say(f"code object attention config3 {e['best']}")
+    _attention_served_equals_linked(served, e, seed=130, H=32)
