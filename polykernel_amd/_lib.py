@@ -62,6 +62,7 @@ SIGNATURES = {
     "pk_parse_gcn_arch_name": (I, [C.c_char_p, C.c_char_p, I]),
     "pk_check_bf16_conversion": (I, [C.POINTER(C.c_ulonglong)]),
     "pk_check_gelu_pairs": (I, [C.POINTER(C.c_ulonglong)]),
+    "pk_check_row_division": (I, [P, I, C.POINTER(C.c_ulonglong)]),
     "launch_rmsnorm": (I, [P, P, P, I, I, F, P]),
     "launch_gelu": (I, [P, P, I, P]),
     "launch_matmul": (I, [P, P, P, I, I, I, P]),

@@ -72,6 +72,17 @@ __device__ __forceinline__ float group_max(float v, float *red) {
   }
 }
 
+__global__ __launch_bounds__(kBlock) void div_check_kernel(const float *__restrict__ ds, int n,
+                                                           unsigned long long *__restrict__ bad) {
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (t >= (int64_t)n * 65536) return;
+  const float d = ds[t >> 16];
+  const float x = bf2f((uint32_t)(t & 0xFFFF));
+  if (!div_row_ok(d) || !div_elem_ok(x)) return;
+  const float want = x / d, got = div_fast(x, d, 1.0f / d);
+  if (__float_as_uint(want) != __float_as_uint(got)) atomicAdd(bad, 1ull);
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm / residual + RMSNorm (vector path: cols % 8 == 0, 16-byte aligned).
 // NW waves cooperate on one row (NW == 1: each wave owns a row, 4 rows per
@@ -115,13 +126,27 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const uint16_t *__r
   }
   ss = group_sum<NW>(ss, red);
   const float rms = sqrtf(ss * inv_cols + eps);
+  // x / rms with the fast exact division when every element of the wave allows it
+  bool ok = div_row_ok(rms);
+#pragma unroll
+  for (int i = 0; i < VPT; ++i)
+    if (lane + i * kLanes < nvec)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ok &= div_elem_ok(v[i][e]);
+  const bool fast = __all(ok);
+  const float rinv = 1.0f / rms;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = lane + i * kLanes;
     if (c < nvec) {
       float o[8];
+      if (fast) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = v[i][e] / rms;
+        for (int e = 0; e < 8; ++e) o[e] = div_fast(v[i][e], rms, rinv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = v[i][e] / rms;
+      }
       if (w) {
         float g[8];
         unpack8(ld16(w + (size_t)c * 8), g);
@@ -547,6 +572,26 @@ int launch_quantize_int8_per_channel(const uint16_t *W, int8_t *Wq, float *scale
   quant_apply_kernel<<<grid_for((int64_t)K * N), kBlock, 0, st>>>(W, scale, Wq, K, N);
   PK_LAUNCH_CHECK("launch_quantize_int8_per_channel");
   return PK_OK;
+}
+
+int pk_check_row_division(const float *divisors, int n, unsigned long long *mismatches) {
+  PK_CHECK_ARG(divisors && mismatches && n >= 0 && n <= 32768, "pk_check_row_division: invalid argument");
+  *mismatches = 0;
+  if (n == 0) return PK_OK;
+  float *dd = nullptr;
+  unsigned long long *bad = nullptr;
+  PK_HIP(hipMalloc(&dd, (size_t)n * sizeof(float)));
+  hipError_t e = hipMalloc(&bad, sizeof *bad);
+  if (e == hipSuccess) e = hipMemcpy(dd, divisors, (size_t)n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(bad, 0, sizeof *bad);
+  if (e == hipSuccess) {
+    div_check_kernel<<<(int)(((int64_t)n * 65536 + kBlock - 1) / kBlock), kBlock>>>(dd, n, bad);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(mismatches, bad, sizeof *bad, hipMemcpyDeviceToHost);
+  (void)hipFree(dd);
+  if (bad) (void)hipFree(bad);
+  return e == hipSuccess ? PK_OK : hip_fail(e, "pk_check_row_division");
 }
 
 }  // extern "C"
