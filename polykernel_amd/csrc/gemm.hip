@@ -211,283 +211,12 @@ int gemm_run(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const u
   }
 }
 
-// ---------------------------------------------------------------------------
-// RMSNorm -> MatMul with the normalised A row-panel resident in LDS
-// (short K: 32 x K bf16 <= 96 KiB).  The block first computes its 32 row RMS
-// values, writes bf16((x / rms) * gamma) into LDS once (exact fp32 division,
-// kernels/cpu/cpu_reference.cpp:16-44), then streams B k-tiles (double
-// buffered) through the same MFMA loop as gemm_kernel.
-// ---------------------------------------------------------------------------
-constexpr int RP_BM = 32, RP_BN = 64, RP_WAVES = 2;
-constexpr int RP_MAX_K = 1536;
-
-__global__ __launch_bounds__(RP_WAVES * 64) void rmsnorm_panel_gemm_kernel(
-    const uint16_t *__restrict__ X, const uint16_t *__restrict__ gamma,
-    const uint16_t *__restrict__ B, uint16_t *__restrict__ C, int M, int N, int K, float inv_cols,
-    float eps) {
-#pragma clang fp contract(off)
-  constexpr int NT = RP_WAVES * 64;
-  constexpr int BN = RP_BN;
-  constexpr int B_CHUNKS = BK * BN / 8, BC = B_CHUNKS / NT;
-  constexpr int BROW_CHUNKS = BN / 8;
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t *Ap = smem;                       // [32][K]
-  uint16_t *Bs0 = smem + RP_BM * K;          // [2][BK*BN]
-  __shared__ float rms_s[RP_BM];
-
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int tn = (N + BN - 1) / BN;
-  const int mt = blockIdx.x / tn, nt = blockIdx.x % tn;
-  const int m0 = mt * RP_BM, n0 = nt * BN;
-  const int kchunks = K >> 3;
-
-  // Row statistics: each wave reduces 16 rows.
-  for (int r = wid; r < RP_BM; r += RP_WAVES) {
-    const int gm = m0 + r;
-    float ss = 0.f;
-    if (gm < M) {
-      for (int c = lane; c < kchunks; c += 64) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a = lo_bf(v[e]), b = hi_bf(v[e]);
-          ss += a * a;
-          ss += b * b;
-        }
-      }
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) rms_s[r] = sqrtf(ss * inv_cols + eps);
-  }
-  __syncthreads();
-  // Normalise the panel into LDS (16-byte chunks swizzled by row within each
-  // aligned group of 8 chunks).
-  for (int q = tid; q < RP_BM * kchunks; q += NT) {
-    const int r = q / kchunks, c = q % kchunks;
-    const int gm = m0 + r;
-    u32x4 o = {0, 0, 0, 0};
-    if (gm < M) {
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
-      u32x4 gv = {0, 0, 0, 0};
-      if (gamma) gv = *reinterpret_cast<const u32x4 *>(gamma + c * 8);
-      const float rms = rms_s[r];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float a = lo_bf(v[e]) / rms, b = hi_bf(v[e]) / rms;
-        if (gamma) {
-          a *= lo_bf(gv[e]);
-          b *= hi_bf(gv[e]);
-        }
-        o[e] = pack_bf(a, b);
-      }
-    }
-    *reinterpret_cast<u32x4 *>(Ap + r * K + ((c ^ (r & 7)) << 3)) = o;
-  }
-
-  u32x4 rb[BC];
-  auto load_b = [&](int kt) {
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int i = 0; i < BC; ++i) {
-      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
-      const int gk = k0 + row, gn = n0 + c * 8;
-      rb[i] = (gk < K && gn < N) ? *reinterpret_cast<const u32x4 *>(B + (size_t)gk * N + gn)
-                                 : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto store_b = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < BC; ++i) {
-      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
-      *reinterpret_cast<u32x4 *>(&Bs0[s * BK * BN + row * BN + ((c ^ swz_b<BN>(row)) << 3)]) = rb[i];
-    }
-  };
-
-  f32x16 acc;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-  const int KT = K / BK;
-  const int grp = lane >> 4, gi = lane & 15;
-  const int b_krow = 8 * (grp >> 1) + (gi >> 2);
-  const int b_col = wid * 32 + 16 * (grp & 1) + 4 * (gi & 3);
-  const int a_row = lane & 31;
-
-  load_b(0);
-  store_b(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) load_b(kt + 1);
-    const uint16_t *bs = Bs0 + cur * BK * BN;
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      const int c = kt * 8 + 2 * s + (lane >> 5);
-      const bf16x8 af = lds_read_a(Ap + a_row * K + ((c ^ (a_row & 7)) << 3));
-      i16x4 h[2];
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int k = 16 * s + 4 * r + b_krow;
-        const int cc = b_col >> 3;
-        h[r] = lds_read_tr(bs + k * BN + ((cc ^ swz_b<BN>(k)) << 3) + (b_col & 7));
-      }
-      short tmp[8] = {h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8, tmp), acc, 0,
-                                                     0, 0);
-    }
-    if (kt + 1 < KT) store_b(cur ^ 1);
-    __syncthreads();
-  }
-  const int n = n0 + wid * 32 + (lane & 31);
-  if (n < N) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = m0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-      if (m < M) C[(size_t)m * N + n] = (uint16_t)f2bf(acc[i]);
-    }
-  }
+// The RMSNorm -> MatMul panel kernels (bodies in gemm_kernels.hpp).
+__global__ __launch_bounds__(RP_WAVES * 64) void rmsnorm_panel_gemm_kernel(PanelArgs a) {
+  rmsnorm_panel_body(a);
 }
-
-// Latency-oriented RMSNorm -> MatMul for short rows (K <= 832, the config-1
-// fragment: a few MB, cache-resident, so one memory round trip dominates).
-// A workgroup of 4 waves owns 32 rows x 64 columns:
-//   - issue the whole 64-column slice of W (K x 64, 128 K bytes) as
-//     buffer_load ... lds DMA into LDS first, then load the 32 x K panel of x
-//     (and gamma) into registers, every load in flight at once;
-//   - 8 lanes per row reduce the sum of squares (shuffles), normalise
-//     x / rms * gamma exactly as the reference and store the bf16 panel in LDS
-//     while W is still arriving;
-//   - wave w computes column block w & 1 over K half w >> 1 (MFMA 32x32x16),
-//     the halves are added in LDS and the tile is stored 16 bytes at a time.
-constexpr int RQ_BM = 32, RQ_BN = 64, RQ_THREADS = 256;
-constexpr int RQ_MAX_K = 832;  // panel 64 K bytes + W slice 128 K bytes <= 160 KiB
-constexpr int RQ_XPT = RQ_MAX_K / 64;  // x chunks (16 B) per thread at most
-
-__global__ __launch_bounds__(RQ_THREADS) void rmsnorm_panel_gemm_fast_kernel(
-    const uint16_t *__restrict__ X, const uint16_t *__restrict__ gamma, const uint16_t *__restrict__ B,
-    uint16_t *__restrict__ C, int M, int N, int K, float inv_cols, float eps) {
-#pragma clang fp contract(off)
-  extern __shared__ __attribute__((aligned(1024))) uint8_t smem8[];
-  uint16_t *Bs = reinterpret_cast<uint16_t *>(smem8);                // [K][64], chunk-swizzled
-  uint16_t *Ap = reinterpret_cast<uint16_t *>(smem8 + (size_t)K * 128);  // [32][K], chunk-swizzled
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tn = (N + RQ_BN - 1) / RQ_BN;
-  const int mt = blockIdx.x / tn, nt = blockIdx.x % tn;
-  const int m0 = mt * RQ_BM, n0 = nt * RQ_BN;
-  const int kchunks = K >> 3;
-
-  // ---- W slice -> LDS: instruction q covers rows 8q..8q+7 (8 chunks each);
-  // lane i fills row 8q + i/8, slot i%8 = logical chunk (i%8) ^ swz_b(row).
-  // Columns past N are clamped onto the last 8 valid ones (never stored).
-  {
-    const pk_u32x4 rs = rsrc_words(B, (uint32_t)((size_t)K * N * 2));
-    const int ninstr = K >> 3;  // 1 KiB each
-    for (int q = wid; q < ninstr; q += RQ_THREADS / 64) {
-      const int row = 8 * q + (lane >> 3), sl = lane & 7;
-      const int col = min(n0 + 8 * (sl ^ swz_b<RQ_BN>(row)), N - 8);
-      dma_lds16(rs, smem8 + q * 1024, (uint32_t)(((size_t)row * N + col) * 2), 0);
-    }
-  }
-
-  // ---- x panel -> registers: thread t owns row t / 8, chunks (t % 8) + 8 j
-  const int r = tid >> 3, c0 = tid & 7;
-  const int gm = m0 + r;
-  const int nxc = (kchunks - c0 + 7) / 8;  // chunks of this thread
-  u32x4 xv[RQ_XPT], gv[RQ_XPT];
-#pragma unroll
-  for (int j = 0; j < RQ_XPT; ++j) {
-    xv[j] = u32x4{0, 0, 0, 0};
-    gv[j] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 (no gamma)
-    if (j < nxc) {
-      const int c = c0 + 8 * j;
-      if (gm < M) xv[j] = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
-      if (gamma) gv[j] = *reinterpret_cast<const u32x4 *>(gamma + c * 8);
-    }
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < RQ_XPT; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float a = lo_bf(xv[j][e]), b = hi_bf(xv[j][e]);
-      ss += a * a;
-      ss += b * b;
-    }
-  ss += __shfl_xor(ss, 1, 64);
-  ss += __shfl_xor(ss, 2, 64);
-  ss += __shfl_xor(ss, 4, 64);
-  const float rms = sqrtf(ss * inv_cols + eps);
-#pragma unroll
-  for (int j = 0; j < RQ_XPT; ++j) {
-    if (j < nxc) {
-      const int c = c0 + 8 * j;
-      u32x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float a = lo_bf(xv[j][e]) / rms, b = hi_bf(xv[j][e]) / rms;
-        if (gamma) {
-          a *= lo_bf(gv[j][e]);
-          b *= hi_bf(gv[j][e]);
-        }
-        o[e] = pack_bf(a, b);
-      }
-      *reinterpret_cast<u32x4 *>(Ap + r * K + ((c ^ (r & 7)) << 3)) = o;
-    }
-  }
-  vm_wait<0>();     // this wave's W loads have landed
-  __syncthreads();  // everyone's W loads and panel stores
-
-  // ---- MFMA: wave -> (column block wid & 1, K half wid >> 1)
-  const int cb = wid & 1, kh = wid >> 1;
-  const int ks = K / 32;  // 16-k steps per half
-  const int grp = lane >> 4, gi = lane & 15;
-  const int b_krow = 8 * (grp >> 1) + (gi >> 2);
-  const int b_col = cb * 32 + 16 * (grp & 1) + 4 * (gi & 3);
-  const int a_row = lane & 31;
-  f32x16 acc;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-  for (int s = kh * ks; s < (kh + 1) * ks; ++s) {
-    const int c = 2 * s + (lane >> 5);
-    const bf16x8 af = lds_read_a(Ap + a_row * K + ((c ^ (a_row & 7)) << 3));
-    i16x4 hb[2];
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int k = 16 * s + 4 * rr + b_krow;
-      const int cc = b_col >> 3;
-      hb[rr] = lds_read_tr(Bs + k * RQ_BN + ((cc ^ swz_b<RQ_BN>(k)) << 3) + (b_col & 7));
-    }
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        af, __builtin_bit_cast(bf16x8, __builtin_shufflevector(hb[0], hb[1], 0, 1, 2, 3, 4, 5, 6, 7)), acc, 0, 0,
-        0);
-  }
-  // ---- add the K halves (fixed order: half 0 + half 1) and store
-  __syncthreads();  // everyone is done reading W: reuse its region (>= 8 KiB)
-  float *red = reinterpret_cast<float *>(Bs);  // [32][64] fp32
-  if (kh == 1) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      red[((i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)) * RQ_BN + cb * 32 + (lane & 31)] = acc[i];
-  }
-  __syncthreads();
-  if (kh == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float *p = red + ((i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)) * RQ_BN + cb * 32 + (lane & 31);
-      *p = acc[i] + *p;
-    }
-  }
-  __syncthreads();
-  {
-    const int rr = tid >> 3, c8 = (tid & 7) * 8;  // 32 rows x 8 chunks of 8 columns
-    const int m = m0 + rr, n = n0 + c8;
-    if (m < M && n < N) {
-      const float *p = red + rr * RQ_BN + c8;
-      const u32x4 o = {pack_bf(p[0], p[1]), pack_bf(p[2], p[3]), pack_bf(p[4], p[5]), pack_bf(p[6], p[7])};
-      *reinterpret_cast<u32x4 *>(C + (size_t)m * N + n) = o;
-    }
-  }
+__global__ __launch_bounds__(RQ_THREADS) void rmsnorm_panel_gemm_fast_kernel(PanelArgs a) {
+  rmsnorm_panel_fast_body(a);
 }
 
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, int rows, int cols,
@@ -521,16 +250,16 @@ int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_
   if (panel_ok && K <= RQ_MAX_K && aligned16(out) && (size_t)K * N * 2 < (size_t(1) << 31)) {
     const int tiles = ((M + RQ_BM - 1) / RQ_BM) * ((N + RQ_BN - 1) / RQ_BN);
     const size_t lds = (size_t)K * 128 + (size_t)RQ_BM * K * 2;
-    rmsnorm_panel_gemm_fast_kernel<<<tiles, RQ_THREADS, lds, st>>>(x, gamma, W, out, M, N, K, 1.0f / (float)K,
-                                                                   eps);
+    rmsnorm_panel_gemm_fast_kernel<<<tiles, RQ_THREADS, lds, st>>>(
+        PanelArgs{x, gamma, W, out, M, N, K, 1.0f / (float)K, eps});
     PK_LAUNCH_CHECK(name);
     return PK_OK;
   }
   if (panel_ok) {
     const int tiles = ((M + RP_BM - 1) / RP_BM) * ((N + RP_BN - 1) / RP_BN);
     const size_t lds = (size_t)RP_BM * K * 2 + 2 * BK * RP_BN * 2;
-    rmsnorm_panel_gemm_kernel<<<tiles, RP_WAVES * 64, lds, st>>>(x, gamma, W, out, M, N, K,
-                                                                 1.0f / (float)K, eps);
+    rmsnorm_panel_gemm_kernel<<<tiles, RP_WAVES * 64, lds, st>>>(
+        PanelArgs{x, gamma, W, out, M, N, K, 1.0f / (float)K, eps});
     PK_LAUNCH_CHECK(name);
     return PK_OK;
   }

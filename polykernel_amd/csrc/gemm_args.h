@@ -1,6 +1,7 @@
-/* gemm_args.h -- kernel arguments of the bf16 GEMM kernels, one layout for the
- * device code (gemm_kernels.hpp) and for hosts that launch an emitted code
- * object with hipModuleLaunchKernel (csrc/runtime/launchers.cpp). */
+/* gemm_args.h -- kernel arguments of the bf16 GEMM and RMSNorm -> MatMul
+ * kernels, one layout for the device code (gemm_kernels.hpp) and for hosts
+ * that launch an emitted code object with hipModuleLaunchKernel
+ * (csrc/runtime/launchers.cpp). */
 #ifndef PK_GEMM_ARGS_H
 #define PK_GEMM_ARGS_H
 
@@ -15,5 +16,15 @@ typedef struct pk_gemm_args {
   const uint16_t *gelu_tab;  /* device GELU table (epilogue 1) */
   int M, N, K;
 } pk_gemm_args;
+
+/* RMSNorm -> MatMul panel kernels: out = bf16(bf16((x / rms) * gamma) @ W) */
+typedef struct pk_panel_args {
+  const uint16_t *X;      /* bf16 [M, K] */
+  const uint16_t *gamma;  /* bf16 [K] or NULL */
+  const uint16_t *B;      /* bf16 [K, N] */
+  uint16_t *C;            /* bf16 [M, N] */
+  int M, N, K;
+  float inv_cols, eps;    /* 1 / K and the RMSNorm epsilon */
+} pk_panel_args;
 
 #endif /* PK_GEMM_ARGS_H */

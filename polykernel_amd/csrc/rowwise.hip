@@ -1,76 +1,13 @@
 // rowwise.hip -- HBM-bound row kernels for gfx950: RMSNorm, residual+RMSNorm,
-// softmax, masked softmax, GELU, KV append, int8 per-channel quantisation.
-//
-// One row per wave (short rows) or per 256-thread block (long rows), the row
-// held in registers so every input byte is read from HBM exactly once; 16-byte
-// vector loads/stores; wave64 shuffle reductions, then one LDS exchange across
-// the block's 4 waves.
-#include "pk_common.hpp"
+// softmax, masked softmax (bodies in rowwise_kernels.hpp), GELU, KV append,
+// int8 per-channel quantisation, and their launchers.
+#include "rowwise_kernels.hpp"
 
 namespace pk {
 
 namespace {
 
-constexpr int kBlock = 256;
-
-struct alignas(16) U4 {
-  uint32_t x, y, z, w;
-};
-
-__device__ __forceinline__ U4 ld16(const void *p) { return *reinterpret_cast<const U4 *>(p); }
-__device__ __forceinline__ void st16(void *p, U4 v) { *reinterpret_cast<U4 *>(p) = v; }
-// 16-byte load of data read exactly once (the rows of x, r, logits, mask):
-// non-temporal, so the stream does not allocate in the caches.  Measured on
-// MI355X: residual+RMSNorm [16384, 8192] 143 -> 123 us, masked softmax
-// 197 -> 169 us (the same hint on the stores made both slower).
-typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ U4 ld16_once(const void *p) {
-  return __builtin_bit_cast(U4, __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4 *>(p)));
-}
-
-__device__ __forceinline__ void unpack8(U4 v, float (&f)[8]) {
-  f[0] = lo_bf(v.x), f[1] = hi_bf(v.x), f[2] = lo_bf(v.y), f[3] = hi_bf(v.y);
-  f[4] = lo_bf(v.z), f[5] = hi_bf(v.z), f[6] = lo_bf(v.w), f[7] = hi_bf(v.w);
-}
-
-__device__ __forceinline__ U4 pack8(const float (&f)[8]) {
-  return U4{pack_bf(f[0], f[1]), pack_bf(f[2], f[3]), pack_bf(f[4], f[5]), pack_bf(f[6], f[7])};
-}
-
-// Sum over the block's waves (NW == 1: just the wave sum).
-template <int NW>
-__device__ __forceinline__ float group_sum(float v, float *red) {
-  v = wave_sum(v);
-  if constexpr (NW == 1) {
-    return v;
-  } else {
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) s += red[i];
-    return s;
-  }
-}
-
-template <int NW>
-__device__ __forceinline__ float group_max(float v, float *red) {
-  v = wave_max(v);
-  if constexpr (NW == 1) {
-    return v;
-  } else {
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float s = red[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) s = fmaxf(s, red[i]);
-    return s;
-  }
-}
+using namespace row;
 
 __global__ __launch_bounds__(kBlock) void div_check_kernel(const float *__restrict__ ds, int n,
                                                            unsigned long long *__restrict__ bad) {
@@ -83,106 +20,15 @@ __global__ __launch_bounds__(kBlock) void div_check_kernel(const float *__restri
   if (__float_as_uint(want) != __float_as_uint(got)) atomicAdd(bad, 1ull);
 }
 
-// ---------------------------------------------------------------------------
-// RMSNorm / residual + RMSNorm (vector path: cols % 8 == 0, 16-byte aligned).
-// NW waves cooperate on one row (NW == 1: each wave owns a row, 4 rows per
-// block).  Each lane keeps VPT 8-element vectors of the row in registers.
-// Arithmetic per kernels/cpu/cpu_reference.cpp:16-44: ss = sum x^2 (fp32),
-// rms = sqrt(ss * (1/cols) + eps), y = bf16((x / rms) [* w]).  With a residual
-// the normalised value is s = bf16(x + r) (tests/golden/golden.py:108-112).
-// ---------------------------------------------------------------------------
+// The row kernels, as the library launches them (bodies in rowwise_kernels.hpp).
 template <int NW, int VPT, bool RESID>
-__global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const uint16_t *__restrict__ x,
-                                                             const uint16_t *__restrict__ r,
-                                                             const uint16_t *__restrict__ w,
-                                                             uint16_t *__restrict__ y, int rows,
-                                                             int cols, float inv_cols, float eps) {
-#pragma clang fp contract(off)
-  __shared__ float red[NW];
-  constexpr int kRowsPerBlock = (NW == 1) ? (kBlock / 64) : 1;
-  constexpr int kLanes = NW * 64;
-  const int row = (NW == 1) ? (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) : blockIdx.x;
-  const int lane = (NW == 1) ? (threadIdx.x & 63) : threadIdx.x;
-  if (row >= rows) return;  // uniform per row-group (NW == 1: per wave)
-  const int nvec = cols >> 3;
-  const size_t base = (size_t)row * cols;
-
-  float v[VPT][8];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = lane + i * kLanes;
-    if (c < nvec) {
-      unpack8(ld16_once(x + base + (size_t)c * 8), v[i]);
-      if constexpr (RESID) {
-        float rv[8];
-        unpack8(ld16_once(r + base + (size_t)c * 8), rv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = bf2f(f2bf(v[i][e] + rv[e]));
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
-    }
-  }
-  ss = group_sum<NW>(ss, red);
-  const float rms = sqrtf(ss * inv_cols + eps);
-  // x / rms with the fast exact division when every element of the wave allows it
-  bool ok = div_row_ok(rms);
-#pragma unroll
-  for (int i = 0; i < VPT; ++i)
-    if (lane + i * kLanes < nvec)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ok &= div_elem_ok(v[i][e]);
-  const bool fast = __all(ok);
-  const float rinv = 1.0f / rms;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = lane + i * kLanes;
-    if (c < nvec) {
-      float o[8];
-      if (fast) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = div_fast(v[i][e], rms, rinv);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = v[i][e] / rms;
-      }
-      if (w) {
-        float g[8];
-        unpack8(ld16(w + (size_t)c * 8), g);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] *= g[e];
-      }
-      st16(y + base + (size_t)c * 8, pack8(o));
-    }
-  }
+__global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(RowArgs a) {
+  rmsnorm_vec_body<NW, VPT, RESID>(a);
 }
 
-// Generic path (any cols / alignment): one block per row, two passes over the
-// row (the second from cache).
 template <bool RESID>
-__global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(
-    const uint16_t *__restrict__ x, const uint16_t *__restrict__ r, const uint16_t *__restrict__ w,
-    uint16_t *__restrict__ y, int rows, int cols, float inv_cols, float eps) {
-#pragma clang fp contract(off)
-  __shared__ float red[kBlock / 64];
-  const int row = blockIdx.x;
-  const size_t base = (size_t)row * cols;
-  float ss = 0.f;
-  for (int c = threadIdx.x; c < cols; c += kBlock) {
-    float s = bf2f(x[base + c]);
-    if constexpr (RESID) s = bf2f(f2bf(s + bf2f(r[base + c])));
-    ss += s * s;
-  }
-  ss = group_sum<kBlock / 64>(ss, red);
-  const float rms = sqrtf(ss * inv_cols + eps);
-  for (int c = threadIdx.x; c < cols; c += kBlock) {
-    float s = bf2f(x[base + c]);
-    if constexpr (RESID) s = bf2f(f2bf(s + bf2f(r[base + c])));
-    float o = s / rms;
-    if (w) o *= bf2f(w[c]);
-    y[base + c] = (uint16_t)f2bf(o);
-  }
+__global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(RowArgs a) {
+  rmsnorm_generic_body<RESID>(a);
 }
 
 template <bool RESID>
@@ -191,15 +37,14 @@ int rmsnorm_dispatch(const uint16_t *x, const uint16_t *r, const uint16_t *w, ui
   PK_CHECK_ARG(x && y && (!RESID || r), "%s: null tensor pointer", name);
   PK_CHECK_ARG(rows >= 0 && cols > 0, "%s: invalid shape rows=%d cols=%d", name, rows, cols);
   if (rows == 0) return PK_OK;
-  const float inv_cols = 1.0f / (float)cols;
+  const RowArgs a{x, RESID ? r : nullptr, w, y, rows, cols, 1.0f / (float)cols, eps};
   const bool vec = (cols % 8 == 0) && aligned16(x) && aligned16(y) && (!RESID || aligned16(r)) &&
                    (!w || aligned16(w));
   const int nvec = cols / 8;
   if (vec && nvec <= 64 * 8) {
     // one wave per row, 4 rows per block
     const dim3 grid((rows + 3) / 4);
-#define PK_RMS_W(VPT)                                                                       \
-  rmsnorm_vec_kernel<1, VPT, RESID><<<grid, kBlock, 0, st>>>(x, r, w, y, rows, cols, inv_cols, eps)
+#define PK_RMS_W(VPT) rmsnorm_vec_kernel<1, VPT, RESID><<<grid, kBlock, 0, st>>>(a)
     if (nvec <= 64) PK_RMS_W(1);
     else if (nvec <= 128) PK_RMS_W(2);
     else if (nvec <= 256) PK_RMS_W(4);
@@ -207,120 +52,25 @@ int rmsnorm_dispatch(const uint16_t *x, const uint16_t *r, const uint16_t *w, ui
 #undef PK_RMS_W
   } else if (vec && nvec <= 256 * 8) {
     const dim3 grid(rows);
-#define PK_RMS_B(VPT)                                                                       \
-  rmsnorm_vec_kernel<4, VPT, RESID><<<grid, kBlock, 0, st>>>(x, r, w, y, rows, cols, inv_cols, eps)
+#define PK_RMS_B(VPT) rmsnorm_vec_kernel<4, VPT, RESID><<<grid, kBlock, 0, st>>>(a)
     if (nvec <= 256 * 4) PK_RMS_B(4);
     else PK_RMS_B(8);
 #undef PK_RMS_B
   } else {
-    rmsnorm_generic_kernel<RESID><<<rows, kBlock, 0, st>>>(x, r, w, y, rows, cols, inv_cols, eps);
+    rmsnorm_generic_kernel<RESID><<<rows, kBlock, 0, st>>>(a);
   }
   PK_LAUNCH_CHECK(name);
   return PK_OK;
 }
 
-// ---------------------------------------------------------------------------
-// Softmax over the last axis.  MODE 0: bf16 input (kernels/cpu/cpu_reference.cpp:107-128);
-// MODE 1: fp32 logits + bf16 additive mask, z = bf16(bf16(x) + mask)
-// (tests/golden/golden.py:115-117).  m = max z, e = exp(z - m), y = bf16(e * (1/sum e)).
-// ---------------------------------------------------------------------------
-template <int MODE>
-__device__ __forceinline__ void load_z8(const void *in, const uint16_t *mask, size_t off,
-                                        float (&z)[8]) {
-  if constexpr (MODE == 0) {
-    unpack8(ld16_once(static_cast<const uint16_t *>(in) + off), z);
-  } else {
-    const float *xf = static_cast<const float *>(in) + off;
-    const U4 a = ld16_once(xf), b = ld16_once(xf + 4);
-    float m[8];
-    unpack8(ld16_once(mask + off), m);
-    const uint32_t raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) z[e] = bf2f(f2bf(bf2f(f2bf(__uint_as_float(raw[e]))) + m[e]));
-  }
-}
-
-template <int MODE>
-__device__ __forceinline__ float load_z1(const void *in, const uint16_t *mask, size_t off) {
-  if constexpr (MODE == 0) {
-    return bf2f(static_cast<const uint16_t *>(in)[off]);
-  } else {
-    const float xb = bf2f(f2bf(static_cast<const float *>(in)[off]));
-    return bf2f(f2bf(xb + bf2f(mask[off])));
-  }
-}
-
 template <int NW, int VPT, int MODE>
-__global__ __launch_bounds__(kBlock) void softmax_vec_kernel(const void *__restrict__ in,
-                                                             const uint16_t *__restrict__ mask,
-                                                             uint16_t *__restrict__ y, int rows,
-                                                             int cols) {
-#pragma clang fp contract(off)
-  __shared__ float red[NW];
-  constexpr int kRowsPerBlock = (NW == 1) ? (kBlock / 64) : 1;
-  constexpr int kLanes = NW * 64;
-  const int row = (NW == 1) ? (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) : blockIdx.x;
-  const int lane = (NW == 1) ? (threadIdx.x & 63) : threadIdx.x;
-  if (row >= rows) return;
-  const int nvec = cols >> 3;
-  const size_t base = (size_t)row * cols;
-
-  float z[VPT][8];
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = lane + i * kLanes;
-    if (c < nvec) {
-      load_z8<MODE>(in, mask, base + (size_t)c * 8, z[i]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, z[i][e]);
-    }
-  }
-  m = group_max<NW>(m, red);
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = lane + i * kLanes;
-    if (c < nvec) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        z[i][e] = expf(z[i][e] - m);
-        s += z[i][e];
-      }
-    }
-  }
-  s = group_sum<NW>(s, red);
-  const float inv = 1.0f / s;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = lane + i * kLanes;
-    if (c < nvec) {
-      float o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = z[i][e] * inv;
-      st16(y + base + (size_t)c * 8, pack8(o));
-    }
-  }
+__global__ __launch_bounds__(kBlock) void softmax_vec_kernel(RowArgs a) {
+  softmax_vec_body<NW, VPT, MODE>(a);
 }
 
 template <int MODE>
-__global__ __launch_bounds__(kBlock) void softmax_generic_kernel(const void *__restrict__ in,
-                                                                 const uint16_t *__restrict__ mask,
-                                                                 uint16_t *__restrict__ y,
-                                                                 int rows, int cols) {
-#pragma clang fp contract(off)
-  __shared__ float red[kBlock / 64];
-  const int row = blockIdx.x;
-  const size_t base = (size_t)row * cols;
-  float m = -INFINITY;
-  for (int c = threadIdx.x; c < cols; c += kBlock) m = fmaxf(m, load_z1<MODE>(in, mask, base + c));
-  m = group_max<kBlock / 64>(m, red);
-  float s = 0.f;
-  for (int c = threadIdx.x; c < cols; c += kBlock) s += expf(load_z1<MODE>(in, mask, base + c) - m);
-  s = group_sum<kBlock / 64>(s, red);
-  const float inv = 1.0f / s;
-  for (int c = threadIdx.x; c < cols; c += kBlock)
-    y[base + c] = (uint16_t)f2bf(expf(load_z1<MODE>(in, mask, base + c) - m) * inv);
+__global__ __launch_bounds__(kBlock) void softmax_generic_kernel(RowArgs a) {
+  softmax_generic_body<MODE>(a);
 }
 
 template <int MODE>
@@ -329,24 +79,25 @@ int softmax_dispatch(const void *in, const uint16_t *mask, uint16_t *y, int rows
   PK_CHECK_ARG(in && y && (MODE == 0 || mask), "%s: null tensor pointer", name);
   PK_CHECK_ARG(rows >= 0 && cols > 0, "%s: invalid shape rows=%d cols=%d", name, rows, cols);
   if (rows == 0) return PK_OK;
+  const RowArgs a{in, MODE == 0 ? nullptr : mask, nullptr, y, rows, cols, 0.f, 0.f};
   const bool vec = (cols % 8 == 0) && aligned16(in) && aligned16(y) && (MODE == 0 || aligned16(mask));
   const int nvec = cols / 8;
   if (vec && nvec <= 64 * 4) {
     const dim3 grid((rows + 3) / 4);
-#define PK_SM_W(VPT) softmax_vec_kernel<1, VPT, MODE><<<grid, kBlock, 0, st>>>(in, mask, y, rows, cols)
+#define PK_SM_W(VPT) softmax_vec_kernel<1, VPT, MODE><<<grid, kBlock, 0, st>>>(a)
     if (nvec <= 64) PK_SM_W(1);
     else if (nvec <= 128) PK_SM_W(2);
     else PK_SM_W(4);
 #undef PK_SM_W
   } else if (vec && nvec <= 256 * 8) {
     const dim3 grid(rows);
-#define PK_SM_B(VPT) softmax_vec_kernel<4, VPT, MODE><<<grid, kBlock, 0, st>>>(in, mask, y, rows, cols)
+#define PK_SM_B(VPT) softmax_vec_kernel<4, VPT, MODE><<<grid, kBlock, 0, st>>>(a)
     if (nvec <= 256 * 2) PK_SM_B(2);
     else if (nvec <= 256 * 4) PK_SM_B(4);
     else PK_SM_B(8);
 #undef PK_SM_B
   } else {
-    softmax_generic_kernel<MODE><<<rows, kBlock, 0, st>>>(in, mask, y, rows, cols);
+    softmax_generic_kernel<MODE><<<rows, kBlock, 0, st>>>(a);
   }
   PK_LAUNCH_CHECK(name);
   return PK_OK;

@@ -29,6 +29,19 @@
 //   The runtime hands these to the library's attention dispatcher
 //   (attention_module.hpp), which makes the linked path's tile-shape, key-split
 //   and workspace decisions and launches the object's entry points.
+//   fused_residual_rmsnorm, fused_softmax_mask (rowwise_kernels.hpp):
+//     pk_row(pk_row_args)          the config's row kernel: vector_width 8 -- one wave per row
+//                                  (block_m 4, grid ceil(rows/4)) or four (block_m 1, grid rows)
+//                                  with `unroll` 16-byte vectors per lane; vector_width 1 -- the
+//                                  generic kernel (grid rows); 256 threads
+//     pk_row_any(pk_row_args)      the generic kernel, for operands the vector kernel cannot take
+//   fused_rmsnorm_matmul (gemm_kernels.hpp, rowwise_kernels.hpp):
+//     pk_panel(pk_panel_args)      block_k = K: the whole-K panel kernel (256 threads); num_warps 2:
+//                                  the double-buffered panel kernel (128 threads); grid
+//                                  ceil(M/32) * ceil(N/64), dynamic LDS as in gemm.hip
+//   or, for a GEMM config (rows too long for a panel): the row normalisation into workspace
+//     pk_row / pk_row_any(pk_row_args) (RMSNorm with gamma at the (M, K) row config), then
+//     pk_gemm(pk_gemm_args)        the config's GEMM kernel
 #include <fcntl.h>
 #include <spawn.h>
 #include <sys/wait.h>
@@ -88,6 +101,31 @@ bool GemmInstance(const Config &c, int epi, std::string &body, int &threads) {
   return true;
 }
 
+// The row kernel a config instantiates (rowwise.hip rmsnorm_dispatch and
+// softmax_dispatch): vector_width 8 -- NW waves per row (block_m 4: one, 1:
+// four) with VPT = unroll vectors per lane; vector_width 1 -- the generic
+// kernel.  `kind` is the third template argument: RMSNorm's residual flag
+// ("true" / "false") or softmax's mode ("1": masked).
+bool RowInstance(const Config &c, bool softmax, const std::string &kind, std::string &body, std::string &any) {
+  const std::string ns = softmax ? "pk::row::softmax_" : "pk::row::rmsnorm_";
+  any = ns + "generic_body<" + kind + ">";
+  if (c.num_warps != 4 || c.block_k != 0) return false;
+  if (c.vector_width == 1) {
+    body = any;
+    return true;
+  }
+  if (c.vector_width != 8 || (c.block_m != 4 && c.block_m != 1) || c.unroll < 1 || c.unroll > 8) return false;
+  body = ns + "vec_body<" + std::to_string(c.block_m == 4 ? 1 : 4) + ", " + std::to_string(c.unroll) + ", " + kind +
+         ">";
+  return true;
+}
+
+std::string RowEntryPoints(const std::string &body, const std::string &any) {
+  return "extern \"C\" __global__ __launch_bounds__(256) void pk_row(pk_row_args a) {\n  " + body +
+         "(a);\n}\n\nextern \"C\" __global__ __launch_bounds__(256) void pk_row_any(pk_row_args a) {\n  " + any +
+         "(a);\n}\n";
+}
+
 std::string Hipcc() {
   if (const char *p = std::getenv("HIPCC")) return p;
   const char *rocm = std::getenv("ROCM_PATH");
@@ -128,11 +166,14 @@ bool RunChild(const std::vector<std::string> &argv, const std::string &log, std:
 bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
   const int epi = Int8Epilogue(e.op), gepi = GemmEpilogue(e.op);
   const bool attention = e.op == "fused_kv_append_attention";
-  if (epi < 0 && gepi < 0 && !attention) {
-    error = "the emitter instantiates the GEMM, int8 and attention ops (matmul, fused_matmul_bias_gelu, "
+  const bool rms = e.op == "fused_residual_rmsnorm", smx = e.op == "fused_softmax_mask";
+  const bool panel = e.op == "fused_rmsnorm_matmul";
+  if (epi < 0 && gepi < 0 && !attention && !rms && !smx && !panel) {
+    error = "the emitter instantiates the ops of the tuning cache (matmul, fused_matmul_bias_gelu, "
             "fused_matmul_bias_residual, matmul_int8, matmul_int8_gelu, matmul_int8_residual, "
-            "fused_kv_append_attention); " +
-            e.op + " is served by the linked kernels";
+            "fused_rmsnorm_matmul, fused_residual_rmsnorm, fused_softmax_mask, fused_kv_append_attention), "
+            "not " +
+            e.op;
     return false;
   }
   const std::vector<Config> cands = autotune::ConfigSpace::Candidates(e.op, e.shape);
@@ -146,6 +187,48 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
     return false;
   }
   const Config &c = e.best;
+  const std::string head = "// Emitted by the polykernel_amd gfx950 emitter for " + runtime::FormatKey(e.gpu, e.op, e.shape) +
+                           "\n// config: " + autotune::ToString(c) + "\n";
+  if (rms || smx) {
+    std::string body, any;
+    if (!RowInstance(c, smx, smx ? "1" : "true", body, any)) {
+      error = "config {" + autotune::ToString(c) + "} has no row kernel template";
+      return false;
+    }
+    source = head + "#include \"rowwise_kernels.hpp\"\n\n" + RowEntryPoints(body, any);
+    return true;
+  }
+  if (panel) {
+    if (c.block_k == e.shape.k && c.num_warps == 4) {  // whole-K panel kernel
+      source = head + "#include \"gemm_kernels.hpp\"\n\n" +
+               "extern \"C\" __global__ __launch_bounds__(256) void pk_panel(pk_panel_args a) {\n"
+               "  pk::gk::rmsnorm_panel_fast_body(a);\n}\n";
+      return true;
+    }
+    if (c.num_warps == 2) {  // double-buffered panel kernel
+      source = head + "#include \"gemm_kernels.hpp\"\n\n" +
+               "extern \"C\" __global__ __launch_bounds__(128) void pk_panel(pk_panel_args a) {\n"
+               "  pk::gk::rmsnorm_panel_body(a);\n}\n";
+      return true;
+    }
+    // rows too long for a panel: RMSNorm (with gamma) at the (M, K) row
+    // config into workspace, then the config's GEMM
+    pk_config rc{};
+    std::string rbody, rany, gbody;
+    int threads = 0;
+    if (pk_op_default_config("fused_residual_rmsnorm", e.shape.m, e.shape.k, 0, &rc) != PK_OK ||
+        !RowInstance(Config{rc.block_m, rc.block_n, rc.block_k, rc.num_warps, rc.vector_width, rc.unroll,
+                            rc.shared_memory_stages},
+                     false, "false", rbody, rany) ||
+        !GemmInstance(c, 0, gbody, threads)) {
+      error = "config {" + autotune::ToString(c) + "} has no RMSNorm -> GEMM kernel template";
+      return false;
+    }
+    source = head + "#include \"gemm_kernels.hpp\"\n#include \"rowwise_kernels.hpp\"\n\n" +
+             RowEntryPoints(rbody, rany) + "\nextern \"C\" __global__ __launch_bounds__(" + std::to_string(threads) +
+             (c.block_k == 32 ? ", 1" : "") + ") void pk_gemm(pk_gemm_args g) {\n  " + gbody + "(g);\n}\n";
+    return true;
+  }
   if (attention) {
     const int dp = c.block_k;
     std::ostringstream s;
@@ -248,7 +331,8 @@ bool EmitCodeObject(runtime::KernelCache &cache, const CacheEntry &e, const std:
   const Config &c = e.best;
   std::ostringstream name;
   name << e.op << "_M" << e.shape.m << "_N" << e.shape.n << "_K" << e.shape.k << "_" << c.block_m << "x" << c.block_n
-       << "x" << c.block_k << "_w" << c.num_warps << "_s" << c.shared_memory_stages << "_v" << c.vector_width;
+       << "x" << c.block_k << "_w" << c.num_warps << "_s" << c.shared_memory_stages << "_v" << c.vector_width
+       << "_u" << c.unroll;
   const std::string base = std::filesystem::absolute(std::filesystem::path(out_dir) / name.str()).string();
   {
     std::ofstream out(base + ".hip");

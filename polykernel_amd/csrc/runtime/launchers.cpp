@@ -19,6 +19,7 @@
 #include "../attention_module.hpp"
 #include "../gemm_args.h"
 #include "../int8_args.h"
+#include "../rowwise_args.h"
 #include "../workspace.hpp"
 
 namespace pk::runtime {
@@ -115,9 +116,9 @@ bool Aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 template <typename Args>
 bool ModuleLaunch(void *fn, unsigned gx, unsigned gy, unsigned threads, void *stream, Args &args, const char *what,
-                  std::string &error) {
+                  std::string &error, unsigned lds_bytes = 0) {
   void *params[] = {&args};
-  const hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), gx, gy, 1, threads, 1, 1, 0,
+  const hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), gx, gy, 1, threads, 1, 1, lds_bytes,
                                              static_cast<hipStream_t>(stream), params, nullptr);
   if (e != hipSuccess) {
     error = std::string("hip launch failed for ") + what + ": " + hipGetErrorString(e);
@@ -243,6 +244,128 @@ LaunchFn CodeObjectGemmLauncher(int epi, std::shared_ptr<ModuleTable> table) {
   };
 }
 
+// The code object cached for an entry, or an error naming how to emit one.
+std::optional<CachedBinary> BinaryOf(const ModuleTable &table, const CacheEntry &e, std::string &error) {
+  std::optional<CachedBinary> bin = table.cache.GetBinary(e.gpu, e.op, e.shape);
+  if (!bin)
+    error = "no code object cached for " + FormatKey(e.gpu, e.op, e.shape) +
+            "; emit one (python -m polykernel_amd.emit)";
+  return bin;
+}
+
+// Launch a row object (pk_row, pk_row_any) on a [rows, cols] argument block
+// as rowwise.hip's dispatchers launch the linked kernels: the config's
+// vector kernel when it is one (vector_width 8) and the operands are 16-byte
+// aligned with cols % 8 == 0, else the generic kernel, one block per row.
+bool RowLaunch(ModuleTable::Loaded *mod, const Config &c, pk_row_args a, void *stream, std::string &error) {
+  const bool vec = c.vector_width == 8 && a.cols % 8 == 0 && Aligned16(a.in) && Aligned16(a.out) &&
+                   (!a.aux || Aligned16(a.aux)) && (!a.gamma || Aligned16(a.gamma));
+  const unsigned grid = vec && c.block_m == 4 ? (unsigned)((a.rows + 3) / 4) : (unsigned)a.rows;
+  return ModuleLaunch(mod->fns[vec ? 0 : 1], grid, 1, 256, stream, a, vec ? "pk_row" : "pk_row_any", error);
+}
+
+// Row-op code objects: residual + RMSNorm and masked softmax.
+LaunchFn CodeObjectRowLauncher(bool softmax, std::shared_ptr<ModuleTable> table) {
+  return [softmax, table](const CacheEntry &e, void *io, std::string &error) {
+    pk_row_args a{};
+    void *stream = nullptr;
+    if (softmax) {
+      SoftmaxMaskIO *p = Cast<SoftmaxMaskIO>(io, error);
+      if (!p) return false;
+      if (!p->logits || !p->mask || !p->out) {
+        error = "fused_softmax_mask code object: null tensor pointer";
+        return false;
+      }
+      if (!CheckEntry(e, p->rows, p->cols, 0, error)) return false;
+      a = pk_row_args{p->logits, p->mask, nullptr, p->out, p->rows, p->cols, 0.f, 0.f};
+      stream = p->stream;
+    } else {
+      ResidualRmsnormIO *p = Cast<ResidualRmsnormIO>(io, error);
+      if (!p) return false;
+      if (!p->x || !p->r || !p->out) {
+        error = "fused_residual_rmsnorm code object: null tensor pointer";
+        return false;
+      }
+      if (!CheckEntry(e, p->rows, p->cols, 0, error)) return false;
+      a = pk_row_args{p->x, p->r, p->gamma, p->out, p->rows, p->cols, 1.0f / (float)p->cols, p->eps};
+      stream = p->stream;
+    }
+    const std::optional<CachedBinary> bin = BinaryOf(*table, e, error);
+    if (!bin) return false;
+    ModuleTable::Loaded *mod = table->Get(*bin, {"pk_row", "pk_row_any"}, error);
+    if (!mod) return false;
+    return RowLaunch(mod, e.best, a, stream, error);
+  };
+}
+
+// RMSNorm -> MatMul code objects.  Panel configs (pk_panel): the operand
+// conditions and the LDS size of gemm.hip fused_rmsnorm_matmul for that
+// kernel.  A GEMM config: RMSNorm into library workspace (pk_row /
+// pk_row_any at the (M, K) row config), then pk_gemm with that config's
+// operand checks.
+LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
+  return [table](const CacheEntry &e, void *io, std::string &error) {
+    RmsnormMatmulIO *p = Cast<RmsnormMatmulIO>(io, error);
+    if (!p) return false;
+    if (!p->x || !p->W || !p->out) {
+      error = "fused_rmsnorm_matmul code object: null tensor pointer";
+      return false;
+    }
+    if (!CheckEntry(e, p->M, p->N, p->K, error)) return false;
+    const Config &c = e.best;
+    const bool fast = c.block_k == p->K && c.num_warps == 4, dbuf = c.num_warps == 2;
+    if (fast || dbuf) {
+      if (!Aligned16(p->x) || !Aligned16(p->W) || (p->gamma && !Aligned16(p->gamma)) ||
+          (fast && !Aligned16(p->out))) {
+        error = "code-object RMSNorm -> MatMul panel config {" + autotune::ToString(c) +
+                "} needs 16-byte aligned x, W, gamma" + (fast ? " and out" : "");
+        return false;
+      }
+      const std::optional<CachedBinary> bin = BinaryOf(*table, e, error);
+      if (!bin) return false;
+      ModuleTable::Loaded *mod = table->Get(*bin, {"pk_panel"}, error);
+      if (!mod) return false;
+      pk_panel_args a{p->x, p->gamma, p->W, p->out, p->M, p->N, p->K, 1.0f / (float)p->K, p->eps};
+      const unsigned tiles = (unsigned)(((p->M + 31) / 32) * ((p->N + 63) / 64));
+      const unsigned lds = fast ? (unsigned)(p->K * 128 + 32 * p->K * 2) : (unsigned)(32 * p->K * 2 + 2 * 64 * 64 * 2);
+      return ModuleLaunch(mod->fns[0], tiles, 1, fast ? 256u : 128u, p->stream, a, "pk_panel", error, lds);
+    }
+    // GEMM config: the row normalisation, then the plain GEMM
+    const bool dma = c.block_k == 32;
+    if ((dma || c.vector_width == 8) && !Aligned16(p->W)) {
+      error = "code-object GEMM config {" + autotune::ToString(c) + "} needs a 16-byte aligned W";
+      return false;
+    }
+    if (dma && !Aligned16(p->out)) {
+      error = "code-object GEMM config {" + autotune::ToString(c) + "} needs a 16-byte aligned out";
+      return false;
+    }
+    pk_config rc{};
+    if (pk_op_default_config("fused_residual_rmsnorm", p->M, p->K, 0, &rc) != PK_OK) {
+      error = std::string("row config: ") + pk_last_error();
+      return false;
+    }
+    const std::optional<CachedBinary> bin = BinaryOf(*table, e, error);
+    if (!bin) return false;
+    ModuleTable::Loaded *mod = table->Get(*bin, {"pk_row", "pk_row_any", "pk_gemm"}, error);
+    if (!mod) return false;
+    WorkspaceLease lease;  // the normalised rows, held until the GEMM is queued
+    if (library_workspace((size_t)p->M * p->K * 2, p->stream, lease) != PK_OK) {
+      error = std::string("library workspace: ") + pk_last_error();
+      return false;
+    }
+    uint16_t *xn = static_cast<uint16_t *>(lease.ptr);
+    const Config row{rc.block_m, rc.block_n, rc.block_k, rc.num_warps, rc.vector_width, rc.unroll,
+                     rc.shared_memory_stages};
+    if (!RowLaunch(mod, row, pk_row_args{p->x, nullptr, p->gamma, xn, p->M, p->K, 1.0f / (float)p->K, p->eps},
+                   p->stream, error))
+      return false;
+    pk_gemm_args g{xn, p->W, p->out, nullptr, nullptr, nullptr, p->M, p->N, p->K};
+    const unsigned tiles = (unsigned)(((p->M + c.block_m - 1) / c.block_m) * ((p->N + c.block_n - 1) / c.block_n));
+    return ModuleLaunch(mod->fns[2], tiles, 1, 64u * c.num_warps, p->stream, g, "pk_gemm", error);
+  };
+}
+
 // Attention code objects: the library's attention dispatcher makes the same
 // tile-shape, key-split, workspace and append decisions as for the linked
 // kernels and launches the object's entry points (attention_module.hpp).
@@ -295,6 +418,9 @@ void RegisterCodeObjectLaunchers(Runtime &rt, const KernelCache &cache) {
   rt.RegisterLauncher("matmul_int8", CodeObjectInt8Launcher(0, table));
   rt.RegisterLauncher("matmul_int8_gelu", CodeObjectInt8Launcher(1, table));
   rt.RegisterLauncher("matmul_int8_residual", CodeObjectInt8Launcher(2, table));
+  rt.RegisterLauncher("fused_residual_rmsnorm", CodeObjectRowLauncher(false, table));
+  rt.RegisterLauncher("fused_softmax_mask", CodeObjectRowLauncher(true, table));
+  rt.RegisterLauncher("fused_rmsnorm_matmul", CodeObjectPanelLauncher(table));
 }
 
 void RegisterBuiltinLaunchers(Runtime &rt) {

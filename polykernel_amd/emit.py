@@ -1,13 +1,14 @@
-"""Emit the gfx950 code objects of a tuning cache's GEMM-family, int8 and attention entries.
+"""Emit the gfx950 code objects of a tuning cache's entries.
 
     python -m polykernel_amd.emit                      # committed cache -> polykernel_amd/tuning/gfx950.d
     python -m polykernel_amd.emit --cache X.json --out DIR
 
-For every GEMM-family, int8 and attention entry of the cache the emitter
+For every entry of the cache (GEMM family, RMSNorm -> MatMul, residual +
+RMSNorm, masked softmax, int8, attention) the emitter
 (csrc/runtime/codegen.cpp) writes a HIP source that instantiates the kernel
-template (gemm_kernels.hpp, int8_stream.hpp, attention_kernels.hpp) at the
-entry's configuration,
-compiles it for gfx950 with hipcc --genco (no GPU needed) and
+template (gemm_kernels.hpp, rowwise_kernels.hpp, int8_stream.hpp,
+attention_kernels.hpp) at the entry's configuration, compiles it for gfx950
+with hipcc --genco (no GPU needed) and
 records the code object's path and FNV-1a hash beside the entry.  The result
 is persisted as DIR/tuning_db.json + DIR/binaries.json (the KernelCache
 persistence format); runtime.Runtime(..., code_objects=True) over
@@ -24,12 +25,13 @@ from pathlib import Path
 from . import runtime as rt
 
 DEFAULT_OUT = rt.TUNING_FILE.with_suffix(".d")
-EMIT_OPS = ("matmul", "fused_matmul_bias_gelu", "fused_matmul_bias_residual",
+EMIT_OPS = ("matmul", "fused_matmul_bias_gelu", "fused_matmul_bias_residual", "fused_rmsnorm_matmul",
+            "fused_residual_rmsnorm", "fused_softmax_mask",
             "matmul_int8", "matmul_int8_gelu", "matmul_int8_residual", "fused_kv_append_attention")
 
 
 def emit(cache_file: Path = rt.TUNING_FILE, out_dir: Path = DEFAULT_OUT, verbose: bool = True) -> int:
-    """Emit every GEMM-family, int8 and attention entry of cache_file into out_dir; returns the count."""
+    """Emit every entry of cache_file into out_dir; returns the count."""
     doc = json.loads(Path(cache_file).read_text())
     entries = [e for e in doc["entries"] if e["op"] in EMIT_OPS and e["validated"]]
     cache = rt.KernelCache()
@@ -46,6 +48,13 @@ CONFORMANCE_OUT = rt.TUNING_FILE.with_name("gfx950.conformance.d")
 GEMM_SHAPE = (200, 264, 256)  # ragged M and N tiles for every tile size
 INT8_SHAPE = (24, 1040, 1024)
 ATT_SQ, ATT_SCACHE, ATT_HEAD_DIMS = 200, 256, (64, 128, 96, 256)
+# row ops: 37 rows (ragged for four rows per workgroup); the widths reach
+# every vector kernel (one wave per row with 1/2/4/8 vectors per lane, four
+# waves with 2/4/8) and the generic kernel (cols % 8 != 0)
+ROW_ROWS, ROW_COLS = 37, (512, 1024, 2048, 4096, 8192, 16384, 1000, 999)
+# RMSNorm -> MatMul: the whole-K panel (ragged M), the double-buffered panel
+# and the long-row path (RMSNorm into workspace, then a GEMM)
+PANEL_SHAPES = ((40, 136, 768), (64, 256, 1536), (72, 264, 2048))
 
 
 def conformance_entries() -> list:
@@ -66,6 +75,13 @@ def conformance_entries() -> list:
         shape = (ATT_SQ, ATT_SCACHE + ATT_SQ, D)
         for cfg in rt.candidates("fused_kv_append_attention", *shape):
             out.append(entry("fused_kv_append_attention", shape, "bf16", cfg))
+    for op, dtype in (("fused_residual_rmsnorm", "bf16"), ("fused_softmax_mask", "fp32")):
+        for cols in ROW_COLS:
+            for cfg in rt.candidates(op, ROW_ROWS, cols, 0):
+                out.append(entry(op, (ROW_ROWS, cols, 0), dtype, cfg))
+    for shape in PANEL_SHAPES:
+        for cfg in rt.candidates("fused_rmsnorm_matmul", *shape):
+            out.append(entry("fused_rmsnorm_matmul", shape, "bf16", cfg))
     cands = rt.candidates("matmul_int8_residual", *INT8_SHAPE)
     split = next(c for c in cands if c["block_k"] < INT8_SHAPE[2])
     for op in ("matmul_int8", "matmul_int8_gelu", "matmul_int8_residual"):
@@ -89,6 +105,11 @@ def _emit_entries(entries, cache, out_dir: Path, verbose: bool):
     and persist it to out_dir (returns the count), else return the list of
     (entry, binary) pairs."""
     objects = Path(out_dir) / "objects"
+    # objects of an earlier emission (other configs, older file names) go
+    if objects.is_dir():
+        for f in objects.iterdir():
+            if f.suffix in (".hip", ".hsaco", ".log"):
+                f.unlink()
 
     # compile in parallel (each a hipcc child process), record in order
     def one(e):

@@ -58,17 +58,56 @@ def test_emit_source_gemm_templates():
 
 
 def test_emit_refuses_other_ops_and_foreign_configs():
-    rows = int8_entry()
-    rows.update(op="fused_residual_rmsnorm", shape={"M": 64, "N": 4096, "K": 0, "dtype": "bf16"},
-                best=rt.default_config("fused_residual_rmsnorm", 64, 4096, 0))
+    other = int8_entry()
+    other.update(op="gelu", shape={"M": 64, "N": 4096, "K": 0, "dtype": "bf16"})
     with pytest.raises(rt.RuntimeError_) as ei:
-        rt.emit_source(rows)
-    assert "served by the linked kernels" in ei.value.message
+        rt.emit_source(other)
+    assert "the emitter instantiates the ops of the tuning cache" in ei.value.message
     bad = int8_entry()
     bad["best"]["block_n"] = 96
     with pytest.raises(rt.RuntimeError_) as ei:
         rt.emit_source(bad)
     assert "is not one the gfx950 kernels implement" in ei.value.message
+
+
+def row_entry(op, rows, cols):
+    dtype = "fp32" if op == "fused_softmax_mask" else "bf16"
+    return {"gpu": "gfx950", "op": op, "shape": {"M": rows, "N": cols, "K": 0, "dtype": dtype},
+            "best": rt.default_config(op, rows, cols, 0), "scored_by": "model", "time_ms": None, "validated": True,
+            "correctness": {"cosine": 1.0, "max_rel_err": 0.0, "pcc": 1.0}}
+
+
+def test_emit_source_row_templates():
+    """Each row config instantiates the kernel rowwise.hip's dispatcher runs
+    for that width (waves per row, vectors per lane), with the generic kernel
+    as the second entry point for unaligned operands."""
+    for op, body, any_ in (("fused_residual_rmsnorm", "rmsnorm_vec_body", "rmsnorm_generic_body<true>"),
+                           ("fused_softmax_mask", "softmax_vec_body", "softmax_generic_body<1>")):
+        kind = "true" if op == "fused_residual_rmsnorm" else "1"
+        widths = {512: f"{body}<1, 1, {kind}>", 1024: f"{body}<1, 2, {kind}>", 8192: f"{body}<4, 4, {kind}>",
+                  16384: f"{body}<4, 8, {kind}>", 999: any_}
+        widths[4096] = f"{body}<1, 8, {kind}>" if op == "fused_residual_rmsnorm" else f"{body}<4, 2, {kind}>"
+        for cols, inst in widths.items():
+            src = rt.emit_source(row_entry(op, 64, cols))
+            assert f"void pk_row(pk_row_args a) {{\n  pk::row::{inst}(a);" in src, (op, cols, src)
+            assert f"void pk_row_any(pk_row_args a) {{\n  pk::row::{any_}(a);" in src, (op, cols)
+            assert '#include "rowwise_kernels.hpp"' in src
+
+
+def test_emit_source_rmsnorm_matmul_templates():
+    """fused_rmsnorm_matmul: the whole-K panel (K <= 832), the double-buffered
+    panel (K <= 1536) and, for longer rows, RMSNorm at the (M, K) row config
+    followed by the config's GEMM."""
+    src = rt.emit_source(gemm_entry("fused_rmsnorm_matmul", 128, 3072, 768))
+    assert "__launch_bounds__(256) void pk_panel(pk_panel_args a) {\n  pk::gk::rmsnorm_panel_fast_body(a);" in src
+    src = rt.emit_source(gemm_entry("fused_rmsnorm_matmul", 64, 256, 1536))
+    assert "__launch_bounds__(128) void pk_panel(pk_panel_args a) {\n  pk::gk::rmsnorm_panel_body(a);" in src
+    e = gemm_entry("fused_rmsnorm_matmul", 72, 264, 2048)
+    src = rt.emit_source(e)
+    assert "pk::row::rmsnorm_vec_body<1, 4, false>(a);" in src and "rmsnorm_generic_body<false>(a);" in src
+    c = e["best"]
+    assert f"gemm_reg_body<{c['block_m']}, {c['block_n']}, 2, 2, 0, true>(g);" in src, src
+    assert "void pk_gemm(pk_gemm_args g)" in src
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None and not __import__("os").path.exists("/opt/rocm/bin/hipcc"),
@@ -113,7 +152,7 @@ def test_code_object_runtime_errors_before_any_device_call(tmp_path):
 
 
 def test_built_code_object_cache_matches_committed_tuning():
-    """build() emitted a code object for every int8 entry of the committed cache."""
+    """build() emitted a code object for every entry of the committed cache."""
     if not rt.CODE_OBJECT_DIR.exists():
         pytest.skip("code objects not built (run __graft_entry__.build())")
     cache = rt.code_object_cache()
@@ -159,6 +198,46 @@ def test_code_object_gemm_launcher_checks_before_any_device_call():
     io.A = 256
     with pytest.raises(rt.RuntimeError_) as ei:
         r.run("fused_matmul_bias_gelu", 4096, 16384, 4096, io)
+    assert "no code object cached" in ei.value.message
+
+
+def test_code_object_row_and_panel_launchers_check_before_any_device_call():
+    """Null operands, a shape other than the entry's, and (panel configs)
+    misaligned operands are refused without touching the device; row objects
+    take unaligned operands on their generic entry point, so for them the
+    next refusal is the missing code object."""
+    cache = rt.KernelCache()
+    cache.put(row_entry("fused_residual_rmsnorm", 64, 4096))
+    cache.put(row_entry("fused_softmax_mask", 64, 4096))
+    cache.put(gemm_entry("fused_rmsnorm_matmul", 128, 3072, 768))
+    r = rt.Runtime(cache, fixed_arch="gfx950", code_objects=True)
+    io = rt.ResidualRmsnormIO(x=256, r=None, gamma=None, out=256, rows=64, cols=4096, eps=1e-6)
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_residual_rmsnorm", 64, 4096, 0, io)
+    assert "null tensor pointer" in ei.value.message
+    io.r = 258
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_residual_rmsnorm", 64, 4096, 0, io)
+    assert "no code object cached" in ei.value.message
+    io.cols = 2048
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_residual_rmsnorm", 64, 4096, 0, io)
+    assert "does not match the selected entry" in ei.value.message
+    sio = rt.SoftmaxMaskIO(logits=256, mask=None, out=256, rows=64, cols=4096)
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_softmax_mask", 64, 4096, 0, sio)
+    assert "null tensor pointer" in ei.value.message
+    pio = rt.RmsnormMatmulIO(x=256, gamma=None, W=None, out=256, M=128, N=3072, K=768, eps=1e-6)
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_rmsnorm_matmul", 128, 3072, 768, pio)
+    assert "null tensor pointer" in ei.value.message
+    pio.W = 264  # not 16-byte aligned
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_rmsnorm_matmul", 128, 3072, 768, pio)
+    assert "16-byte aligned" in ei.value.message
+    pio.W = 256
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run("fused_rmsnorm_matmul", 128, 3072, 768, pio)
     assert "no code object cached" in ei.value.message
 
 

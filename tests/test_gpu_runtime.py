@@ -552,9 +552,11 @@ def test_code_objects_serve_config2_gemms_bit_identical(gpu, op, M, N, Kd, epi):
 def test_conformance_code_objects_bit_identical(gpu):
     """Every kernel template the emitter instantiates (the GEMM family's DMA
     ring at both depths and the register-staged tiles at both vector widths,
-    with every epilogue; int8 with and without a K split), served from its
-    code object, equals the linked kernel at the same configuration bit for
-    bit (ragged M and N tiles; null bias for the residual op included)."""
+    with every epilogue; int8 with and without a K split; every row kernel of
+    residual + RMSNorm and masked softmax; the RMSNorm -> MatMul panels and
+    long-row path; attention), served from its code object, equals the
+    linked kernel at the same configuration bit for bit (ragged M and N
+    tiles; null bias for the residual op included)."""
     import torch
 
     from polykernel_amd import emit
@@ -572,6 +574,12 @@ def test_conformance_code_objects_bit_identical(gpu):
         cache.put(e)
         cache.put_binary("gfx950", op, M, N, Kd, sh["dtype"], line["so_path"], line["kernel_hash"])
         served = rt.Runtime(cache, code_objects=True)
+        if op in ("fused_residual_rmsnorm", "fused_softmax_mask"):
+            _row_served_equals_linked(served, e, seed=140 + i)
+            continue
+        if op == "fused_rmsnorm_matmul":
+            _panel_served_equals_linked(served, e, seed=150 + i)
+            continue
         out, direct = _empty_bf16((M, N)), _empty_bf16((M, N))
         a = to_dev(synth.normal_bf16((M, Kd), 110 + i))
         r = to_dev(synth.normal_bf16((M, N), 111 + i))
@@ -603,6 +611,62 @@ def test_conformance_code_objects_bit_identical(gpu):
             direct = kernels.matmul_int8_ex(epi, a, wq, s, residual=rr, config=cfg)
             torch.cuda.synchronize()
             assert torch.equal(out.view(torch.int16), direct.view(torch.int16)), (op, cfg)
+
+
+def _row_served_equals_linked(served, e, seed):
+    """A residual + RMSNorm or masked-softmax call served from its code object
+    equals the linked launcher bit for bit: with 16-byte aligned operands (the
+    config's kernel; RMSNorm with and without gamma) and with every operand
+    one element past alignment (both paths take the generic kernel)."""
+    import torch
+
+    lib = _lib.load()
+    op, rows, cols = e["op"], e["shape"]["M"], e["shape"]["N"]
+    n = rows * cols + 8
+    for off in (0, 1):
+        outs = [torch.zeros(n, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+        if op == "fused_softmax_mask":
+            lg = torch.from_numpy(synth.normal_f32((n,), seed, 2.0)).cuda()
+            mk = to_dev(synth.mask_bf16((n,), seed + 1, 0.1))
+            io = rt.SoftmaxMaskIO(logits=_ptr(lg[off:]), mask=_ptr(mk[off:]), out=_ptr(outs[0][off:]), rows=rows,
+                                  cols=cols, stream=_stream())
+            served.run(op, rows, cols, 0, io)
+            _lib.check(lib.launch_fused_softmax_mask(_ptr(lg[off:]), _ptr(mk[off:]), _ptr(outs[1][off:]), rows, cols,
+                                                     _stream()), op)
+        else:
+            x, r = to_dev(synth.normal_bf16((n,), seed)), to_dev(synth.normal_bf16((n,), seed + 1))
+            for gamma in (to_dev(synth.normal_bf16((cols + 8,), seed + 2, 0.1, 1.0)), None):
+                g = gamma[off:] if gamma is not None else None
+                io = rt.ResidualRmsnormIO(x=_ptr(x[off:]), r=_ptr(r[off:]), gamma=_ptr(g), out=_ptr(outs[0][off:]),
+                                          rows=rows, cols=cols, eps=1e-6, stream=_stream())
+                served.run(op, rows, cols, 0, io)
+                _lib.check(lib.launch_fused_residual_rmsnorm(_ptr(x[off:]), _ptr(r[off:]), _ptr(g),
+                                                             _ptr(outs[1][off:]), rows, cols, 1e-6, _stream()), op)
+                torch.cuda.synchronize()
+                assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (op, cols, off, gamma is None)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (op, cols, off)
+
+
+def _panel_served_equals_linked(served, e, seed):
+    """An RMSNorm -> MatMul call served from its code object (a panel kernel,
+    or RMSNorm into workspace followed by the GEMM) equals the linked
+    launcher bit for bit, with gamma and without."""
+    import torch
+
+    lib = _lib.load()
+    M, N, K = e["shape"]["M"], e["shape"]["N"], e["shape"]["K"]
+    x = to_dev(synth.normal_bf16((M, K), seed))
+    w = to_dev(synth.normal_bf16((K, N), seed + 1, 1.0 / math.sqrt(K)))
+    for gamma in (to_dev(synth.normal_bf16((K,), seed + 2, 0.1, 1.0)), None):
+        out, direct = _empty_bf16((M, N)), _empty_bf16((M, N))
+        io = rt.RmsnormMatmulIO(x=_ptr(x), gamma=_ptr(gamma), W=_ptr(w), out=_ptr(out), M=M, N=N, K=K, eps=1e-6,
+                                stream=_stream())
+        served.run("fused_rmsnorm_matmul", M, N, K, io)
+        _lib.check(lib.launch_fused_rmsnorm_matmul_gamma(_ptr(x), _ptr(gamma), _ptr(w), _ptr(direct), M, N, K, 1e-6,
+                                                         _stream()), "fused_rmsnorm_matmul")
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), direct.view(torch.int16)), (M, N, K, e["best"], gamma is None)
 
 
 def _attention_served_equals_linked(served, e, seed, B=1, H=4):
