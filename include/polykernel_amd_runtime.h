@@ -136,9 +136,8 @@ typedef struct pk_runtime pk_runtime;
  * fixed detector reporting that arch (for tests). */
 PK_API pk_runtime *pk_runtime_create(const pk_kernel_cache *cache, const char *fixed_arch);
 PK_API void pk_runtime_destroy(pk_runtime *rt);
-/* As pk_runtime_create; with PK_RUNTIME_CODE_OBJECTS in `flags` the GEMM
- * family (matmul, fused_matmul_bias_gelu, fused_matmul_bias_residual) and the
- * int8 ops are served from the code objects the cache holds for their entries
+/* As pk_runtime_create; with PK_RUNTIME_CODE_OBJECTS in `flags` every op is
+ * served from the code object the cache holds for its entry
  * (pk_emit_code_object) instead of the linked kernels. */
 #define PK_RUNTIME_CODE_OBJECTS 1
 PK_API pk_runtime *pk_runtime_create_ex(const pk_kernel_cache *cache, const char *fixed_arch, int flags);

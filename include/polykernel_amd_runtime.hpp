@@ -379,13 +379,13 @@ using KvAppendAttentionIO = pk_kv_append_attention_io;
 // config is one the kernels implement, then launches through the C-ABI.
 PK_API void RegisterBuiltinLaunchers(Runtime &runtime);
 
-// Serve the GEMM family (matmul, fused_matmul_bias_gelu,
-// fused_matmul_bias_residual) and matmul_int8, matmul_int8_gelu and
-// matmul_int8_residual from the code objects `cache` holds for their entries
-// (codegen::EmitCodeObject): the
-// object is loaded once (hash-checked) and launched with
-// hipModuleLaunchKernel.  An entry without a cached code object is an error.
-// `cache` must outlive the runtime.
+// Serve every built-in op (the GEMM family, fused_rmsnorm_matmul,
+// fused_residual_rmsnorm, fused_softmax_mask, fused_kv_append_attention and
+// the three int8 ops) from the code objects `cache` holds for their entries
+// (codegen::EmitCodeObject): the object is loaded once (hash-checked) and
+// launched with hipModuleLaunchKernel, with the linked path's launch
+// geometry and operand checks for the entry's config.  An entry without a
+// cached code object is an error.  `cache` must outlive the runtime.
 PK_API void RegisterCodeObjectLaunchers(Runtime &runtime, const KernelCache &cache);
 
 // ---- code objects -------------------------------------------------------------
@@ -414,10 +414,12 @@ class PK_API CodeObject {
 
 namespace pk::codegen {
 
-// The gfx950 HIP source of a tuned int8 entry: the streaming kernel's
-// template instantiated at the entry's config behind extern "C" entry points
-// pk_int8_stream / pk_int8_reduce.  Other ops are served by the linked
-// kernels and are refused.
+// The gfx950 HIP source of a tuned entry: the op's kernel template
+// instantiated at the entry's config behind fixed extern "C" entry points
+// (pk_gemm; pk_row / pk_row_any; pk_panel; pk_fa_fused / pk_fa_combine or
+// pk_att / pk_att_unaligned / pk_att_combine / pk_kv_append; pk_int8_stream /
+// pk_int8_reduce).  An op outside the tuning cache's ops, or a config the
+// kernels do not implement for the shape, is refused.
 PK_API bool EmitSource(const autotune::CacheEntry &entry, std::string &source, std::string &error);
 // hipcc --genco for gfx950 (the library's flags) in a child process; the
 // kernel headers are found under csrc_dir.

@@ -212,8 +212,8 @@ CODE_OBJECTS = 1  # PK_RUNTIME_CODE_OBJECTS
 class Runtime:
     """detect -> select -> serve over a KernelCache, with every built-in
     launcher registered.  fixed_arch=None detects the HIP device.  With
-    code_objects=True the int8 ops are served from the code objects the cache
-    holds for their entries (emit_code_object), loaded with hipModuleLoad."""
+    code_objects=True every op is served from the code object the cache holds
+    for its entry (emit_code_object), loaded with hipModuleLoad."""
 
     def __init__(self, cache: KernelCache, fixed_arch: Optional[str] = None, code_objects: bool = False):
         self._lib = _lib.load()
@@ -242,7 +242,7 @@ CSRC_DIR = _lib._PKG / "csrc"
 
 
 def emit_source(entry: dict) -> str:
-    """gfx950 HIP source instantiating a tuned int8 entry's kernel."""
+    """gfx950 HIP source instantiating a tuned entry's kernel template at its config."""
     _call("emit_source", _lib.load().pk_emit_source(_s(json.dumps(entry))))
     return _lib.last_text()
 

@@ -1,7 +1,8 @@
-"""The gfx950 emitter on the CPU: a tuned int8 entry becomes HIP source that
-instantiates the streaming kernel at its config, hipcc --genco cross-compiles
-it to an ELF code object, and the KernelCache records and re-checks its
-FNV-1a hash (the .hsaco half of lib/Runtime/KernelCache.cpp:296-392)."""
+"""The gfx950 emitter on the CPU: a tuned entry becomes HIP source that
+instantiates its op's kernel template at the entry's config, hipcc --genco
+cross-compiles it to an ELF code object, and the KernelCache records and
+re-checks its FNV-1a hash (the .hsaco half of lib/Runtime/KernelCache.cpp:296-392);
+the code-object launchers refuse bad argument blocks before any device call."""
 from __future__ import annotations
 
 import json
