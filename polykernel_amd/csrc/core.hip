@@ -286,10 +286,7 @@ int pk_check_bf16_conversion(unsigned long long *mismatches) {
   return PK_OK;
 }
 
-// The bare arch token of a gcnArchName: the first "gfx" followed by a digit,
-// through the run of lower-case letters and digits after it
-// ("gfx950:sramecc+:xnack-" -> "gfx950"); "" when there is none
-// (lib/Runtime/DeviceDetect.cpp:28-50 of the reference).
+// Runs gelu_pair_selfcheck_kernel; the mismatch count goes to *mismatches.
 int pk_check_gelu_pairs(unsigned long long *mismatches) {
   PK_CHECK_ARG(mismatches, "pk_check_gelu_pairs: null argument");
   const uint16_t *tab = nullptr;
@@ -308,6 +305,10 @@ int pk_check_gelu_pairs(unsigned long long *mismatches) {
   return PK_OK;
 }
 
+// The bare arch token of a gcnArchName: from the first "gfx", when a digit
+// follows it, through the run of lower-case letters and digits after it
+// ("gfx950:sramecc+:xnack-" -> "gfx950"); "" otherwise
+// (lib/Runtime/DeviceDetect.cpp:28-50 of the reference).
 int pk_parse_gcn_arch_name(const char *name, char *buf, int buf_len) {
   if (!name || !buf || buf_len <= 0) {
     set_error("pk_parse_gcn_arch_name: null argument");
