@@ -705,6 +705,24 @@ def _attention_served_equals_linked(served, e, seed, B=1, H=4):
     assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
 
 
+@pytest.mark.parametrize("op,M,N,Kd", [("fused_rmsnorm_matmul", 128, 3072, 768),
+                                       ("fused_residual_rmsnorm", 16384, 8192, 0),
+                                       ("fused_softmax_mask", 16384, 8192, 0)])
+def test_code_objects_serve_configs_1_4a_4b_bit_identical(gpu, op, M, N, Kd):
+    """The committed config-1, 4a and 4b entries served from their emitted
+    code objects equal the linked launchers bit for bit at full size."""
+    assert rt.CODE_OBJECT_DIR.exists(), "code objects missing: run __graft_entry__.build()"
+    cache = rt.code_object_cache()
+    served = rt.Runtime(cache, code_objects=True)
+    e = served.resolve(op, M, N, Kd)
+    assert cache.get_binary("gfx950", op, M, N, Kd, e["shape"]["dtype"]) is not None
+    _say(f"code object {op} {M}x{N}x{Kd} {e['best']}")
+    if op == "fused_rmsnorm_matmul":
+        _panel_served_equals_linked(served, e, seed=160)
+    else:
+        _row_served_equals_linked(served, e, seed=170)
+
+
 def test_code_objects_serve_config3_attention_bit_identical(gpu):
     """The committed config-3 attention entry (B1 H32 D128, 3584 + 512) served
     from its emitted code object equals the linked kernels bit for bit."""
