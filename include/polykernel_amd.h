@@ -68,7 +68,8 @@ PK_API int pk_check_gelu_pairs(unsigned long long *mismatches);
 /* Self-check of the row kernels' division x / d (d the row's RMS): for each of
  * the n divisors (n <= 32768) and every bf16 numerator x inside the fast
  * path's range, counts the outputs that differ from the device's IEEE
- * division.  Expected 0. */
+ * division; and, for every bf16 code, counts a disagreement between the packed
+ * magnitude range test and the float one.  Expected 0. */
 PK_API int pk_check_row_division(const float *divisors, int n, unsigned long long *mismatches);
 
 /* ---- reference entry points (same names and argument order) ------------ */

@@ -926,23 +926,47 @@ __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
   ss += __shfl_xor(ss, 2, 64);
   ss += __shfl_xor(ss, 4, 64);
   const float rms = sqrtf(ss * inv_cols + eps);
+  // x / rms: the three-operation exact division (div_fast) when every
+  // numerator and divisor of the wave is in its range, else the IEEE division
+  DivSpan span;
+  if (gm < M) {
 #pragma unroll
-  for (int j = 0; j < RQ_XPT; ++j) {
-    if (j < nxc) {
-      const int c = c0 + 8 * j;
-      u32x4 o;
+    for (int j = 0; j < RQ_XPT; ++j)
+      if (j < nxc)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float a = lo_bf(xv[j][e]) / rms, b = hi_bf(xv[j][e]) / rms;
-        if (gamma) {
-          a *= lo_bf(gv[j][e]);
-          b *= hi_bf(gv[j][e]);
-        }
-        o[e] = pack_bf(a, b);
-      }
-      *reinterpret_cast<u32x4 *>(Ap + r * K + ((c ^ (r & 7)) << 3)) = o;
-    }
+        for (int e = 0; e < 4; ++e) div_span_add(span, xv[j][e]);
   }
+  const bool fast = __all(div_row_ok(rms) && div_span_ok(span));
+  auto normalise = [&](auto fast_c) __attribute__((always_inline)) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    const float rinv = FAST ? 1.0f / rms : 0.f;
+#pragma unroll
+    for (int j = 0; j < RQ_XPT; ++j) {
+      if (j < nxc) {
+        const int c = c0 + 8 * j;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float a, b;
+          if constexpr (FAST) {
+            a = div_fast(lo_bf(xv[j][e]), rms, rinv);
+            b = div_fast(hi_bf(xv[j][e]), rms, rinv);
+          } else {
+            a = lo_bf(xv[j][e]) / rms;
+            b = hi_bf(xv[j][e]) / rms;
+          }
+          if (gamma) {
+            a *= lo_bf(gv[j][e]);
+            b *= hi_bf(gv[j][e]);
+          }
+          o[e] = pack_bf(a, b);
+        }
+        *reinterpret_cast<u32x4 *>(Ap + r * K + ((c ^ (r & 7)) << 3)) = o;
+      }
+    }
+  };
+  if (fast) normalise(std::true_type{});
+  else normalise(std::false_type{});
   vm_wait<0>();     // this wave's W loads have landed
   __syncthreads();  // everyone's W loads and panel stores
 

@@ -57,9 +57,7 @@ inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3
 // step underflows or overflows, which d in [2^-30, 2^30] and |x| in
 // [2^-64, 2^64] guarantee.  A wave whose elements all qualify takes three
 // operations per element instead of the ~10 of the division sequence;
-// otherwise the wave divides every element.  (The RMSNorm->MatMul panel kernels
-// keep the division: in those latency-bound kernels the vote and branch cost
-// more than they save -- config 1 9.6 -> 10.7 us.)  Checked against IEEE
+// otherwise the wave divides every element.  Checked against IEEE
 // division for all 65536 bf16 numerators x 2000 divisors on the CPU
 // (tests/cpp/row_division_check.c; 20000 divisors in a longer run, no
 // mismatch) and x 4096 divisors on the device (pk_check_row_division).
@@ -72,6 +70,24 @@ __device__ __forceinline__ bool div_elem_ok(float x) {
 __device__ __forceinline__ float div_fast(float x, float d, float y) {
   const float q = x * y;
   return fmaf(fmaf(-q, d, x), y, q);
+}
+// The element test on bf16 numerators held two per 32-bit word, at 1.5
+// operations per element: bf16 magnitudes (bits & 0x7FFF) order like unsigned
+// integers, and |x| in [2^-64, 2^64) is exactly magnitude bits in [0x1F80,
+// 0x5F80) (zero of either sign falls outside).  DivSpan keeps the running
+// minimum and maximum magnitude of both halves with packed 16-bit integer
+// min / max; div_span_ok tests the span once.
+typedef unsigned short pk_u16x2 __attribute__((ext_vector_type(2)));
+struct DivSpan {
+  pk_u16x2 lo = {0xFFFF, 0xFFFF}, hi = {0, 0};
+};
+__device__ __forceinline__ void div_span_add(DivSpan &sp, uint32_t two_bf16) {
+  const pk_u16x2 m = __builtin_bit_cast(pk_u16x2, two_bf16 & 0x7FFF7FFFu);
+  sp.lo = __builtin_elementwise_min(sp.lo, m);
+  sp.hi = __builtin_elementwise_max(sp.hi, m);
+}
+__device__ __forceinline__ bool div_span_ok(const DivSpan &sp) {
+  return (sp.lo.x < sp.lo.y ? sp.lo.x : sp.lo.y) >= 0x1F80 && (sp.hi.x > sp.hi.y ? sp.hi.x : sp.hi.y) < 0x5F80;
 }
 
 // Per-device compact GELU table (see gelu_bits), built on the device on first

@@ -14,7 +14,18 @@ __global__ __launch_bounds__(kBlock) void div_check_kernel(const float *__restri
   const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (t >= (int64_t)n * 65536) return;
   const float d = ds[t >> 16];
-  const float x = bf2f((uint32_t)(t & 0xFFFF));
+  const uint32_t code = (uint32_t)(t & 0xFFFF);
+  const float x = bf2f(code);
+  if ((t >> 16) == 0) {
+    // once per numerator code: the packed magnitude test (DivSpan) accepts
+    // exactly the codes with 2^-64 <= |x| < 2^64, whether the code is paired
+    // with itself or with an in-range code (1.0) in its 32-bit word
+    DivSpan self, mixed;
+    div_span_add(self, code | (code << 16));
+    div_span_add(mixed, code | (0x3F80u << 16));
+    const bool want = div_elem_ok(x) && fabsf(x) < 0x1p64f;
+    if (div_span_ok(self) != want || div_span_ok(mixed) != want) atomicAdd(bad, 1ull);
+  }
   if (!div_row_ok(d) || !div_elem_ok(x)) return;
   const float want = x / d, got = div_fast(x, d, 1.0f / d);
   if (__float_as_uint(want) != __float_as_uint(got)) atomicAdd(bad, 1ull);

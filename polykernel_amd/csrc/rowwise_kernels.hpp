@@ -109,11 +109,19 @@ __device__ __forceinline__ void rmsnorm_vec_body(const RowArgs &a) {
 
   float v[VPT][8];
   float ss = 0.f;
+  DivSpan span;  // magnitudes of the numerators (without a residual: the loaded words)
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = lane + i * kLanes;
     if (c < nvec) {
-      unpack8(ld16_once(x + base + (size_t)c * 8), v[i]);
+      const U4 xw = ld16_once(x + base + (size_t)c * 8);
+      unpack8(xw, v[i]);
+      if constexpr (!RESID) {
+        div_span_add(span, xw.x);
+        div_span_add(span, xw.y);
+        div_span_add(span, xw.z);
+        div_span_add(span, xw.w);
+      }
       if constexpr (RESID) {
         float rv[8];
         unpack8(ld16_once(r + base + (size_t)c * 8), rv);
@@ -128,11 +136,15 @@ __device__ __forceinline__ void rmsnorm_vec_body(const RowArgs &a) {
   const float rms = sqrtf(ss * inv_cols + eps);
   // x / rms with the fast exact division when every element of the wave allows it
   bool ok = div_row_ok(rms);
+  if constexpr (RESID) {
 #pragma unroll
-  for (int i = 0; i < VPT; ++i)
-    if (lane + i * kLanes < nvec)
+    for (int i = 0; i < VPT; ++i)
+      if (lane + i * kLanes < nvec)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ok &= div_elem_ok(v[i][e]);
+        for (int e = 0; e < 8; ++e) ok &= div_elem_ok(v[i][e]);
+  } else {
+    ok &= div_span_ok(span);
+  }
   const bool fast = __all(ok);
   const float rinv = 1.0f / rms;
 #pragma unroll

@@ -3,6 +3,7 @@
 // divisors (structured, the ends of the fast range, and random):
 //   y = RN(1/d); q = RN(x y); e = fma(-q, d, x); result = fma(e, y, q)
 // on the fast path (d in [2^-30, 2^30], |x| in [2^-64, 2^64]), x / d otherwise.
+// Also checks the packed range test that selects the fast path (check_span).
 // Build with -ffp-contract=off so every multiply and add rounds separately.
 // Exit status 0 when no result differs.
 #include <math.h>
@@ -24,9 +25,45 @@ static float fastdiv(float x, float d, float y) {
   return fmaf(e, y, q);
 #endif
 }
+// The kernels' packed range test (pk_common.hpp DivSpan): a 32-bit word of
+// two bf16 numerators qualifies when both magnitudes (bits & 0x7FFF) lie in
+// [0x1F80, 0x5F80).  It must accept exactly the words whose two values satisfy
+// 2^-64 <= |x| < 2^64 (the float test).
+static int span_ok(uint32_t w) {
+  const uint32_t lo = w & 0x7FFFu, hi = (w >> 16) & 0x7FFFu;
+  const uint32_t mn = lo < hi ? lo : hi, mx = lo > hi ? lo : hi;
+#ifdef PK_PLANT_SPAN_BOUND
+  return mn >= 0x1F80u && mx <= 0x5F80u;  /* a deliberately wrong bound: 2^64 accepted */
+#else
+  return mn >= 0x1F80u && mx < 0x5F80u;
+#endif
+}
+static int float_ok(uint16_t b) {
+  const float a = fabsf(bf(b));
+  return a >= 0x1p-64f && a < 0x1p64f;
+}
+static unsigned long long check_span(void) {
+  unsigned long long bad = 0;
+  for (uint32_t b = 0; b < 65536; ++b)
+    for (uint32_t k = 0; k < 65536; k += 251) {  // every code against 262 partners, both orders
+      const uint32_t c = (b * 40503u + k) & 0xFFFFu;
+      const int want = float_ok((uint16_t)b) && float_ok((uint16_t)c);
+      if (span_ok(b | (c << 16)) != want || span_ok(c | (b << 16)) != want) {
+        if (bad < 5) printf("span mismatch %04x %04x\n", b, c);
+        ++bad;
+      }
+    }
+  for (uint32_t b = 0; b < 65536; ++b)  // every code with itself and with 1.0
+    if (span_ok(b | (b << 16)) != float_ok((uint16_t)b) || span_ok(b | (0x3F80u << 16)) != float_ok((uint16_t)b))
+      ++bad;
+  return bad;
+}
 int main(int argc, char **argv) {
   long n = argc > 1 ? atol(argv[1]) : 2000;
   unsigned long long bad = 0, checked = 0, fastpath = 0;
+  const unsigned long long span_bad = check_span();
+  printf("span mismatches %llu\n", span_bad);
+  bad += span_bad;
   srand(12345);
   for (long i = 0; i < n; ++i) {
     float d;

@@ -8,7 +8,10 @@ compares the method with IEEE x / d for all 65536 bf16 numerators x 2000
 divisors.  GPU: pk_check_row_division compares the device implementation
 with the device's own IEEE division over every bf16 numerator for 4096
 divisors.  A method that skipped the correction step (q = x * RN(1/d)) fails
-both: the CPU check plants that mistake and expects mismatches.
+both: the CPU check plants that mistake and expects mismatches.  The packed
+range test that picks the fast path (DivSpan: two bf16 magnitudes per word,
+packed 16-bit min / max) is checked against the float test for every code,
+on the CPU (with a planted off-by-one bound that must fail) and on the device.
 """
 from __future__ import annotations
 
@@ -34,10 +37,15 @@ def _build(tmp_path, extra=()):
     return exe
 
 
+def _summary(r):
+    """The division sweep's closing line: "checked N, fast path F, mismatches M"."""
+    return r.stdout.strip().splitlines()[-1]
+
+
 def test_division_method_matches_ieee_on_cpu(tmp_path):
     exe = _build(tmp_path)
     r = subprocess.run([str(exe), "2000"], capture_output=True, text=True, timeout=120)
-    assert r.returncode == 0 and "mismatches 0" in r.stdout, r.stdout
+    assert r.returncode == 0 and _summary(r).endswith("mismatches 0") and "span mismatches 0" in r.stdout, r.stdout
 
 
 def test_check_detects_a_missing_correction(tmp_path):
@@ -45,7 +53,15 @@ def test_check_detects_a_missing_correction(tmp_path):
     (the check can fail)."""
     exe = _build(tmp_path, ["-DPK_PLANT_NO_CORRECTION"])
     r = subprocess.run([str(exe), "200"], capture_output=True, text=True, timeout=120)
-    assert r.returncode != 0 and "mismatches 0" not in r.stdout, r.stdout
+    assert r.returncode != 0 and not _summary(r).endswith("mismatches 0"), r.stdout
+
+
+def test_check_detects_a_wrong_range_bound(tmp_path):
+    """The packed range test with its upper bound off by one (2^64 accepted)
+    must report mismatches."""
+    exe = _build(tmp_path, ["-DPK_PLANT_SPAN_BOUND"])
+    r = subprocess.run([str(exe), "1"], capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "span mismatches 0" not in r.stdout, r.stdout
 
 
 @pytest.mark.gpu
