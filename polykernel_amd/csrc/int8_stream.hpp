@@ -101,7 +101,10 @@ __device__ __forceinline__ void reduce8_body(const float *partial, int splits, i
 //   W part: [64 rows][NT chunks of 16 B] int8.  DMA lane i of instruction q
 //     fills slot c = 64q + i, i.e. row c / NT, slot c % NT, which holds
 //     logical chunk (c % NT) ^ xw(row): the XOR (power-of-two NT) makes the
-//     8 rows of a transpose read hit distinct banks; odd NT needs none.
+//     8 rows of a transpose read hit distinct banks, and (NT 8 and 16) gives
+//     rows 8-15 the banks rows 0-7 leave free, since the two 16-lane groups
+//     of a 32-lane LDS pass read 8 rows each (45 % -> 6.5 % bank-conflict
+//     cycles); odd NT needs none.
 //   A part: [16*MT rows][8 chunks of 16 B] bf16 (64 k), slot s of row r holds
 //     chunk s ^ (r & 7) (each wave loads its own copy from L2).
 // ds_read_b64_tr_b8 turns 8 rows x 16 columns of int8 into the MFMA B
@@ -125,7 +128,8 @@ template <int NT>
 __device__ __forceinline__ int i8s_xw(int row) {
   if constexpr (NT == 2) return (row >> 2) & 1;
   else if constexpr (NT == 4) return (row >> 1) & 3;
-  else if constexpr (NT == 8 || NT == 16) return row & 7;
+  else if constexpr (NT == 8) return (row & 7) ^ ((row >> 3) & 1);
+  else if constexpr (NT == 16) return (row & 7) | ((row >> 3) & 1) << 3;
   else return 0;  // odd NT: rows already fall on distinct banks
 }
 
