@@ -104,7 +104,8 @@ PK_API int launch_fused_rmsnorm_matmul(const uint16_t *input, const uint16_t *we
 PK_API int launch_fused_matmul_bias_gelu(const uint16_t *a, const uint16_t *b, const uint16_t *bias,
                                   uint16_t *output, int M, int N, int K, void *stream);
 
-/* Causal/non-causal SDPA, Q [B,H,S_q,D], K/V [B,H,S_kv,D], O [B,H,S_q,D].
+/* Causal/non-causal SDPA, Q [B,H,S_q,D], K/V [B,H,S_kv,D], O [B,H,S_q,D],
+ * any D <= 1024 (larger: PK_ERR_UNSUPPORTED).
  * Query i attends to keys j <= S_kv - S_q + i when causal.
  * Replaces launch_attention_prefill, kernels/generated/attention_prefill.cu:169-172. */
 PK_API int launch_attention_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O,

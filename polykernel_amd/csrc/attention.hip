@@ -19,7 +19,8 @@
 // that key order, so P never leaves registers and the rescale by
 // exp(m_old - m_new) is a per-lane multiply.
 //
-// Work split (attention_kernel, any D <= 256): a workgroup = 4 waves x 32
+// Work split (attention_kernel, any D <= 256; head dims up to 1024 take
+// attention_wide_kernel, which splits the dims over its waves): a workgroup = 4 waves x 32
 // queries of one (b,h); K/V tiles are double-buffered in LDS.  When queries
 // alone do not fill the chip the key range is split (flash-decoding style)
 // and att_combine_kernel merges the fp32 partials in split order.  Head dims
@@ -44,6 +45,11 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttArgs g) {
 template <int DP>
 __global__ __launch_bounds__(256) void att_combine_kernel(AttArgs g) {
   att_combine_body<DP>(g);
+}
+
+template <bool ALIGNED>
+__global__ __launch_bounds__(AW_THREADS, 1) void attention_wide_kernel(AttArgs g) {
+  att_wide_body<ALIGNED>(g);
 }
 
 template <int DP, int QG, bool FUSED>
@@ -109,6 +115,42 @@ int attention_dp(AttArgs g, hipStream_t st, const AttModule *mod) {
     const int grid = (int)std::min<int64_t>((total + 255) / 256, 8192);
     if (mod) return run_module(mod->att_combine, "pk_att_combine", grid, 256, g, st);
     att_combine_kernel<DP><<<grid, 256, 0, st>>>(g);
+    PK_LAUNCH_CHECK("att_combine_kernel");
+  }
+  return PK_OK;
+}
+
+// Head dims 257..1024: 32 queries x 32 keys per step, 4 waves splitting the
+// head dims (att_wide_body), key splits merged as for attention_dp.
+int attention_wide(AttArgs g, hipStream_t st, const AttModule *mod) {
+  const bool aligned = (g.D % 8 == 0) && aligned16(g.Q) && aligned16(g.K) && aligned16(g.V);
+  g.q_tiles = (g.S_q + AW_BQ - 1) / AW_BQ;
+  const int kv_tiles = (g.S_kv + AW_BKV - 1) / AW_BKV;
+  g.splits = pick_splits(g.BH, g.q_tiles, kv_tiles);
+  WorkspaceLease lease;  // held until the combine kernel is queued
+  if (g.splits > 1) {
+    const size_t rows = (size_t)g.BH * g.S_q;
+    const size_t bytes_o = (size_t)g.splits * rows * AW_DMAX * sizeof(float);
+    const size_t bytes = bytes_o + (size_t)g.splits * rows * 2 * sizeof(float);
+    int rc = library_workspace(bytes, st, lease);
+    if (rc) return rc;
+    g.part_o = static_cast<float *>(lease.ptr);
+    g.part_ml = reinterpret_cast<float *>(static_cast<char *>(lease.ptr) + bytes_o);
+  }
+  const int blocks = g.BH * g.q_tiles * g.splits;
+  if (mod) {
+    int rc = run_module(aligned ? mod->att : mod->att_unaligned, "pk_att", blocks, AW_THREADS, g, st);
+    if (rc) return rc;
+  } else {
+    if (aligned) attention_wide_kernel<true><<<blocks, AW_THREADS, 0, st>>>(g);
+    else attention_wide_kernel<false><<<blocks, AW_THREADS, 0, st>>>(g);
+    PK_LAUNCH_CHECK("attention_wide_kernel");
+  }
+  if (g.splits > 1) {
+    const int64_t total = (int64_t)g.BH * g.S_q * g.D;
+    const int grid = (int)std::min<int64_t>((total + 255) / 256, 8192);
+    if (mod) return run_module(mod->att_combine, "pk_att_combine", grid, 256, g, st);
+    att_combine_kernel<AW_DMAX><<<grid, 256, 0, st>>>(g);
     PK_LAUNCH_CHECK("att_combine_kernel");
   }
   return PK_OK;
@@ -218,17 +260,24 @@ int attention_fa(FaArgs a, int D, int qg, hipStream_t st, const AttModule *mod) 
 // Configs of attention as descriptors: the flash kernel's two tile shapes
 // for D 64 / 128 ({queries, keys per step, D, 8 waves, 16-byte vectors,
 // D/16 MFMA k-steps per product, K/V ring slots}), the generic kernel
-// otherwise.  unroll = MFMA k-steps of one query-key product.
+// otherwise: up to D 256 {128 queries, 64 keys, padded D, 4 waves, vector
+// width, padded D / 16, 1}, above it the wide kernel {32 queries, 32 keys,
+// 1024, 4 waves, vector width, 16 k-steps per wave, 1}.  unroll = MFMA
+// k-steps of one query-key product (per wave for the wide kernel).
 pk_config fa_config(int qg, int D) {
   return pk_config{fa_bq(qg), fa_bkv(qg), D, FA_WAVES, 8, D / 16, FA_RING / (2 * fa_bkv(qg) * D * 2)};
 }
 bool generic_attention_config(int D, pk_config *out) {
+  if (D > 256) {
+    *out = pk_config{AW_BQ, AW_BKV, AW_DMAX, AW_WAVES, D % 8 == 0 ? 8 : 1, AW_DC / 16, 1};
+    return true;
+  }
   const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
   *out = pk_config{AT_BQ, AT_BKV, dp, AT_WAVES, D % 8 == 0 ? 8 : 1, dp / 16, 1};
   return true;
 }
 int attention_configs(int S_q, int S_kv, int D, pk_config *out, int cap) {
-  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 256) return 0;
+  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > AW_DMAX) return 0;
   pk_config c[2];
   int n = 0;
   if (D == 64 || D == 128) {
@@ -243,7 +292,7 @@ int attention_configs(int S_q, int S_kv, int D, pk_config *out, int cap) {
 // The built-in choice.  The shape key has no batch x heads: this assumes 32
 // (the headline configuration's and the autotuner's default).
 bool attention_config(int S_q, int S_kv, int D, pk_config *out) {
-  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > 256) return false;
+  if (S_q <= 0 || S_kv <= 0 || D <= 0 || D > AW_DMAX) return false;
   if (D == 64 || D == 128) *out = fa_config(fa_default_qg(32, S_q), D);
   else generic_attention_config(D, out);
   return true;
@@ -285,7 +334,8 @@ int attention_run(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint1
   if (D <= 64) return attention_dp<64>(g, st, mod);
   if (D <= 128) return attention_dp<128>(g, st, mod);
   if (D <= 256) return attention_dp<256>(g, st, mod);
-  set_error("attention: head dim %d > 256 is not supported", D);
+  if (D <= AW_DMAX) return attention_wide(g, st, mod);
+  set_error("attention: head dim %d > 1024 is not supported", D);
   return PK_ERR_UNSUPPORTED;
 }
 
@@ -300,8 +350,8 @@ int fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc, con
   PK_CHECK_ARG((int64_t)S_cache + S_q <= cache_capacity,
                "launch_fused_kv_append_attention: S_cache + S_q = %lld exceeds cache_capacity %d",
                (long long)S_cache + S_q, cache_capacity);
-  if (D > 256) {  // refused before the append touches the caches
-    set_error("launch_fused_kv_append_attention: head dim %d > 256 is not supported", D);
+  if (D > AW_DMAX) {  // refused before the append touches the caches
+    set_error("launch_fused_kv_append_attention: head dim %d > 1024 is not supported", D);
     return PK_ERR_UNSUPPORTED;
   }
   const int64_t BH = (int64_t)B * H;

@@ -303,6 +303,227 @@ __device__ __forceinline__ void att_body(AttArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide heads (256 < D <= 1024, attention_prefill.cu:166-180 accepts any D up
+// to 1024).  A workgroup of 4 waves owns 32 queries of one (b,h); wave w owns
+// head dims [256 w, 256 w + 256).  Per step of 32 keys: the K and V rows go to
+// LDS (zero past D), each wave forms the partial scores of its dims
+// (S^T = K Q^T, 16 MFMA k-steps) into LDS, then every wave adds the partials
+// in wave order, runs the online softmax of att_body on the full scores (the
+// same values in every wave) and accumulates P V for its own dims.  Waves
+// whose dims lie past D skip the products.  Key splits and their merge as in
+// att_body (att_combine_body<AW_DMAX>).
+constexpr int AW_BQ = 32, AW_BKV = 32, AW_DMAX = 1024, AW_DC = 256, AW_WAVES = 4;
+constexpr int AW_THREADS = AW_WAVES * 64;
+
+template <bool ALIGNED>
+__device__ __forceinline__ void att_wide_body(AttArgs g) {
+  constexpr int DS = AW_DC / 16;   // k-steps of a wave's partial scores
+  constexpr int DB = AW_DC / 32;   // d blocks of a wave's P V product
+  constexpr int KS = AW_DMAX + 8;  // LDS row strides (elements): consecutive K rows
+  constexpr int VS = AW_DMAX + 16; // 16 B apart in the banks, V rows 32 B
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[AW_BKV * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[AW_BKV * VS];
+  __shared__ float Sp[AW_WAVES][16][64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, grp = lane >> 4, gi = lane & 15;
+  int b = blockIdx.x;
+  const int per_bh = g.q_tiles * g.splits;
+  const int total = g.BH * per_bh;
+  if ((total & 7) == 0) b = (b & 7) * (total >> 3) + (b >> 3);
+  const int bh = b / per_bh;
+  const int rem = b % per_bh;
+  const int qt = rem / g.splits, split = rem % g.splits;
+  const int q0 = qt * AW_BQ;
+  const int my_q = q0 + (lane & 31);
+
+  const int off = g.S_kv - g.S_q;
+  int kv_end = g.S_kv;
+  if (g.causal) kv_end = min(g.S_kv, max(0, off + q0 + AW_BQ));
+  const int ntiles = (kv_end + AW_BKV - 1) / AW_BKV;
+  const int tps = (ntiles + g.splits - 1) / g.splits;
+  const int t_begin = split * tps;
+  const int t_end = min(ntiles, t_begin + tps);
+
+  const int nc = (g.D + AW_DC - 1) / AW_DC;  // waves that own dims
+  const int dw = wid * AW_DC;                // this wave's first dim
+  const bool active = wid < nc;
+  const int cpr = nc * AW_DC / 8;            // 16-byte chunks of an LDS row in use
+
+  const size_t kvbase = (size_t)bh * g.kv_rows * g.D;
+  const uint16_t *Kp = g.K + kvbase;
+  const uint16_t *Vp = g.V + kvbase;
+
+  // Q^T fragments of this wave's dims: query lane % 32, d = dw + 16 ds + 8 h + 0..7
+  bf16x8 qf[DS];
+  {
+    const uint16_t *qrow = g.Q + ((size_t)bh * g.S_q + min(my_q, g.S_q - 1)) * g.D;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const int d = dw + 16 * ds + 8 * h;
+      u32x4 v = {0, 0, 0, 0};
+      if (my_q < g.S_q) {
+        if constexpr (ALIGNED) {
+          if (d < g.D) v = *reinterpret_cast<const u32x4 *>(qrow + d);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (d + e < g.D) v[e >> 1] |= (uint32_t)qrow[d + e] << (16 * (e & 1));
+        }
+      }
+      qf[ds] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  // K and V rows [k0, k0 + 32) into LDS, zero past kv_end and past D
+  auto load_tile = [&](int t) {
+    const int k0 = t * AW_BKV;
+    for (int q = tid; q < AW_BKV * cpr; q += AW_THREADS) {
+      const int row = q / cpr, d = 8 * (q % cpr), key = k0 + row;
+      u32x4 a = {0, 0, 0, 0}, v = {0, 0, 0, 0};
+      if (key < kv_end && d < g.D) {
+        const size_t o = (size_t)key * g.D + d;
+        if constexpr (ALIGNED) {
+          a = *reinterpret_cast<const u32x4 *>(Kp + o);
+          v = *reinterpret_cast<const u32x4 *>(Vp + o);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if (d + e < g.D) {
+              a[e >> 1] |= (uint32_t)Kp[o + e] << (16 * (e & 1));
+              v[e >> 1] |= (uint32_t)Vp[o + e] << (16 * (e & 1));
+            }
+          }
+        }
+      }
+      *reinterpret_cast<u32x4 *>(&Ks[row * KS + d]) = a;
+      *reinterpret_cast<u32x4 *>(&Vs[row * VS + d]) = v;
+    }
+  };
+
+  f32x16 acc_o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_o[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const int q_limit = g.causal ? (off + my_q) : (g.S_kv - 1);
+
+  for (int t = t_begin; t < t_end; ++t) {
+    __syncthreads();  // the previous step's reads of Ks, Vs and Sp are done
+    load_tile(t);
+    __syncthreads();
+    const int k0 = t * AW_BKV;
+    if (active) {
+      // partial S^T over this wave's dims (32 keys x 32 queries)
+      f32x16 sp;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sp[e] = 0.f;
+      const int row = lane & 31;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const u32x4 kv = *reinterpret_cast<const u32x4 *>(&Ks[row * KS + dw + 16 * ds + 8 * h]);
+        sp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kv), qf[ds], sp, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Sp[wid][e][lane] = sp[e];
+    }
+    __syncthreads();
+    if (!active) continue;  // wave-uniform; every wave still meets the barriers above
+
+    // ---- full scores (partials added in wave order), scale, mask, online softmax
+    float tmax = -INFINITY;
+    float s[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float v = Sp[0][i][lane];
+      for (int w = 1; w < nc; ++w) v += Sp[w][i][lane];
+      const int key = k0 + (i >> 2) * 8 + h * 4 + (i & 3);
+      v *= g.scale;
+      if (key > q_limit || key >= kv_end) v = -INFINITY;
+      s[i] = v;
+      tmax = fmaxf(tmax, v);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __expf(m_run - m_use);
+    // p = p_hi + p_lo with both halves bf16 for the P V product (as att_body)
+    float psum = 0.f;
+    uint32_t phi[8], plo[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = __expf(s[i] - m_use);
+      const float p1 = __expf(s[i + 1] - m_use);
+      psum += p0 + p1;
+      const uint32_t h0 = f2bf(p0), h1 = f2bf(p1);
+      const uint32_t l0 = f2bf(p0 - bf2f(h0)), l1 = f2bf(p1 - bf2f(h1));
+      phi[i >> 1] = h0 | (h1 << 16);
+      plo[i >> 1] = l0 | (l1 << 16);
+    }
+    psum += __shfl_xor(psum, 32, 64);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_o[db][e] *= alpha;
+
+    // ---- O^T += V^T (P_hi + P_lo)^T for this wave's dims, 2 steps of 16 keys
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const u32x4 hv4 = {phi[4 * st + 0], phi[4 * st + 1], phi[4 * st + 2], phi[4 * st + 3]};
+      const u32x4 lv4 = {plo[4 * st + 0], plo[4 * st + 1], plo[4 * st + 2], plo[4 * st + 3]};
+      const bf16x8 pb_hi = __builtin_bit_cast(bf16x8, hv4);
+      const bf16x8 pb_lo = __builtin_bit_cast(bf16x8, lv4);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        i16x4 hv[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int key = st * 16 + 8 * r + 4 * h + (gi >> 2);
+          const int d = dw + db * 32 + 16 * (grp & 1) + 4 * (gi & 3);
+          hv[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(&Vs[key * VS + d]));
+        }
+        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(hv[0], hv[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb_hi, acc_o[db], 0, 0, 0);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb_lo, acc_o[db], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- output: acc_o[db][i] -> d = dw + db*32 + (i/4)*8 + h*4 + i%4, query my_q
+  if (!active || my_q >= g.S_q) return;
+  const size_t orow = (size_t)bh * g.S_q + my_q;
+  if (g.splits == 1) {
+    const float inv = 1.0f / l_run;
+    uint16_t *op = g.O + orow * g.D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = dw + db * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+        if (d < g.D) op[d] = (uint16_t)f2bf(acc_o[db][i] * inv);
+      }
+  } else {
+    float *po = g.part_o + ((size_t)split * g.BH * g.S_q + orow) * AW_DMAX;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = dw + db * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+        if (d < g.D) po[d] = acc_o[db][i];
+      }
+    if (wid == 0 && h == 0) {
+      float *pml = g.part_ml + ((size_t)split * g.BH * g.S_q + orow) * 2;
+      pml[0] = m_run;
+      pml[1] = l_run;
+    }
+  }
+}
+
 template <int DP>
 __device__ __forceinline__ void att_combine_body(AttArgs g) {
   const int64_t rows = (int64_t)g.BH * g.S_q;

@@ -23,7 +23,8 @@
 //   fused_kv_append_attention (attention_kernels.hpp), the flash kernel's tile shapes (num_warps 8):
 //     pk_fa_fused(pk_fa_args)      the flash kernel with the in-place append, 512 threads
 //     pk_fa_combine(pk_fa_args)    the merge of key splits, 256 threads
-//   and the generic kernel (num_warps 4, block_k = padded head dim):
+//   and the generic kernel (num_warps 4, block_k = padded head dim; 1024:
+//   the wide-head kernel for head dims 257..1024):
 //     pk_att / pk_att_unaligned(pk_att_args), pk_att_combine(pk_att_args),
 //     pk_kv_append(pk_kv_append_args)
 //   The runtime hands these to the library's attention dispatcher
@@ -242,10 +243,14 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
         << "extern \"C\" __global__ __launch_bounds__(256) void pk_fa_combine(pk_fa_args g) {\n"
         << "  pk::att::fa_combine_body<" << dp << ">(g);\n}\n";
     } else {
-      s << "extern \"C\" __global__ __launch_bounds__(256) void pk_att(pk_att_args g) {\n"
-        << "  pk::att::att_body<" << dp << ", true>(g);\n}\n\n"
-        << "extern \"C\" __global__ __launch_bounds__(256) void pk_att_unaligned(pk_att_args g) {\n"
-        << "  pk::att::att_body<" << dp << ", false>(g);\n}\n\n"
+      // block_k 1024: the wide-head kernel (head dims split over the waves, one wave per SIMD)
+      const bool wide = dp == 1024;
+      const std::string body = wide ? "pk::att::att_wide_body<" : "pk::att::att_body<" + std::to_string(dp) + ", ";
+      const std::string bounds = wide ? "256, 1" : "256";
+      s << "extern \"C\" __global__ __launch_bounds__(" << bounds << ") void pk_att(pk_att_args g) {\n"
+        << "  " << body << "true>(g);\n}\n\n"
+        << "extern \"C\" __global__ __launch_bounds__(" << bounds << ") void pk_att_unaligned(pk_att_args g) {\n"
+        << "  " << body << "false>(g);\n}\n\n"
         << "extern \"C\" __global__ __launch_bounds__(256) void pk_att_combine(pk_att_args g) {\n"
         << "  pk::att::att_combine_body<" << dp << ">(g);\n}\n\n"
         << "extern \"C\" __global__ __launch_bounds__(256) void pk_kv_append(pk_kv_append_args a) {\n"

@@ -47,7 +47,7 @@ def emit(cache_file: Path = rt.TUNING_FILE, out_dir: Path = DEFAULT_OUT, verbose
 CONFORMANCE_OUT = rt.TUNING_FILE.with_name("gfx950.conformance.d")
 GEMM_SHAPE = (200, 264, 256)  # ragged M and N tiles for every tile size
 INT8_SHAPE = (24, 1040, 1024)
-ATT_SQ, ATT_SCACHE, ATT_HEAD_DIMS = 200, 256, (64, 128, 96, 256)
+ATT_SQ, ATT_SCACHE, ATT_HEAD_DIMS = 200, 256, (64, 128, 96, 256, 512, 300)
 # row ops: 37 rows (ragged for four rows per workgroup); the widths reach
 # every vector kernel (one wave per row with 1/2/4/8 vectors per lane, four
 # waves with 2/4/8) and the generic kernel (cols % 8 != 0)

@@ -570,16 +570,34 @@ def test_attention_prefill_wide_heads(gpu, oracle, B, H, Sq, Skv, D, causal):
     assert _att_bound_bad(oracle, got, want, q, k, v, causal) == 0, rep
 
 
-def test_attention_head_dim_above_256_refused(gpu):
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 2, 100, 300, 512), (2, 2, 64, 200, 320), (1, 1, 33, 70, 300),
+                                          (1, 1, 32, 1024, 1024), (1, 3, 65, 130, 1000), (1, 1, 40, 40, 264)])
+def test_attention_prefill_head_dims_above_256(gpu, oracle, B, H, Sq, Skv, D, causal):
+    """Head dims 257..1024 (attention_prefill.cu:166-180 accepts D <= 1024):
+    the wide kernel splits the dims over its 4 waves (one to four of them
+    active), aligned and unaligned D (300), ragged query and key counts, and a
+    one-tile grid whose key range is split over 8 workgroups and merged."""
+    _say(f"attention D>256 {B},{H},{Sq},{Skv},{D} causal={causal}")
+    q, k, v = rng_bf16((B, H, Sq, D), 86), rng_bf16((B, H, Skv, D), 87), rng_bf16((B, H, Skv, D), 88)
+    got = from_dev(K().attention_prefill(to_dev(q), to_dev(k), to_dev(v), None, causal))
+    want = oracle.attention_prefill(q, k, v, None, causal)
+    rep = mt.report(got, want)
+    _say(f"attention D>256: {rep}")
+    assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+    assert _att_bound_bad(oracle, got, want, q, k, v, causal) == 0, rep
+
+
+def test_attention_head_dim_above_1024_refused(gpu):
     from polykernel_amd._lib import PK_ERR_UNSUPPORTED, PolyKernelError
 
-    q = to_dev(rng_bf16((1, 1, 8, 264), 79))
+    q = to_dev(rng_bf16((1, 1, 8, 1032), 79))
     with pytest.raises(PolyKernelError) as e:
         K().attention_prefill(q, q, q, None, True)
-    assert e.value.code == PK_ERR_UNSUPPORTED and "256" in e.value.message
+    assert e.value.code == PK_ERR_UNSUPPORTED and "1024" in e.value.message
 
 
-@pytest.mark.parametrize("Sc,D", [(192, 128), (201, 128), (128, 64), (130, 64), (160, 256)])
+@pytest.mark.parametrize("Sc,D", [(192, 128), (201, 128), (128, 64), (130, 64), (160, 256), (96, 384)])
 def test_fused_kv_append_attention_flash_path(gpu, oracle, Sc, D):
     """In-place append fused into the flash kernel (S_cache a multiple of its
     64-key step) and the fallback (separate append kernels) otherwise; the
@@ -643,11 +661,12 @@ def test_fused_kv_append_attention_config3_heads(gpu, oracle):
                           True) == 0, rep
 
 
-@pytest.mark.parametrize("Sc,Sn,D", [(256, 160, 128), (384, 100, 64)])
+@pytest.mark.parametrize("Sc,Sn,D", [(256, 160, 128), (384, 100, 64), (100, 60, 512)])
 def test_fused_kv_append_attention_every_config(gpu, oracle, Sc, Sn, D):
     """Each configuration pk_op_configs lists (the flash kernel's 128 x 64 and
-    64 x 128 tile shapes) through pk_fused_kv_append_attention_config: the
-    appended cache bit-exact, outputs within the attention error model."""
+    64 x 128 tile shapes for D 64 / 128; the wide kernel's 32 x 32 for D 512)
+    through pk_fused_kv_append_attention_config: the appended cache
+    bit-exact, outputs within the attention error model."""
     import ctypes
 
     import torch
@@ -658,8 +677,9 @@ def test_fused_kv_append_attention_every_config(gpu, oracle, Sc, Sn, D):
     B, H = 1, 4
     cfgs = (_lib.Config * 8)()
     n = lib.pk_op_configs(b"fused_kv_append_attention", Sn, Sc + Sn, D, cfgs, 8)
-    assert n == 2, n
-    assert {(cfgs[i].block_m, cfgs[i].block_n) for i in range(n)} == {(128, 64), (64, 128)}
+    shapes = {(128, 64), (64, 128)} if D in (64, 128) else {(32, 32)}
+    assert n == len(shapes), n
+    assert {(cfgs[i].block_m, cfgs[i].block_n) for i in range(n)} == shapes
     q = rng_bf16((B, H, Sn, D), 110)
     kn, vn = rng_bf16((B, H, Sn, D), 111), rng_bf16((B, H, Sn, D), 112)
     kc, vc = rng_bf16((B, H, Sc, D), 113), rng_bf16((B, H, Sc, D), 114)
