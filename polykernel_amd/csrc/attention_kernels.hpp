@@ -743,18 +743,30 @@ __device__ __forceinline__ void fa_body(FaArgs g) {
   struct Pw {
     bf16x8 hi[2], lo[2];
   };
-  auto softmax = [&](auto mask_c, int step, f32x16 sc, Pw &pw, bool &resc) __attribute__((always_inline)) -> float {
+  auto row_max = [&](const f32x16 &x) __attribute__((always_inline)) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, x[i]);
+    return fmaxf(m, __shfl_xor(m, 32, 64));
+  };
+  // pre_max: the block's row max when the caller has it (unmasked blocks)
+  auto softmax = [&](auto mask_c, int step, f32x16 sc, Pw &pw, bool &resc, const float *pre_max = nullptr)
+      __attribute__((always_inline)) -> float {
     constexpr bool MASKED = decltype(mask_c)::value;
     float tmax = -INFINITY;
+    if (!MASKED && pre_max) {
+      tmax = *pre_max;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if constexpr (MASKED) {
-        const int key = kb0_of(step) + (i >> 2) * 8 + h * 4 + (i & 3);
-        if (key > q_limit || key >= kv_end) sc[i] = -INFINITY;
+      for (int i = 0; i < 16; ++i) {
+        if constexpr (MASKED) {
+          const int key = kb0_of(step) + (i >> 2) * 8 + h * 4 + (i & 3);
+          if (key > q_limit || key >= kv_end) sc[i] = -INFINITY;
+        }
+        tmax = fmaxf(tmax, sc[i]);
       }
-      tmax = fmaxf(tmax, sc[i]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     float alpha = 1.f;
     resc = __any((tmax - m_run) * c2 > 8.0f);  // also true for the first block (m_run = -inf)
     if (resc) {
@@ -885,7 +897,11 @@ __device__ __forceinline__ void fa_body(FaArgs g) {
   // The DMA of the iteration goes out in four parts between the LDS reads of
   // the score and P V products and the softmax: issued in one burst after
   // the barrier, the loads of all 8 waves queue at the texture unit and
-  // stall the waves' compute behind them.
+  // stall the waves' compute behind them.  The row max of the next step's
+  // scores is taken at the end of the iteration (sc_max), where it overlaps
+  // the P V products, so the next softmax starts with its exponentials
+  // (config 3: 57.30 -> 57.05 us median over 40 interleaved rounds).
+  float sc_max = -INFINITY;
   auto hot = [&](int s, int kslot, int vslot, int islot) __attribute__((always_inline)) {
     wait_barrier(s);
     const f32x16 nxt = qk(kslot);
@@ -895,13 +911,15 @@ __device__ __forceinline__ void fa_body(FaArgs g) {
     pv(pw_prev, vslot, 1, 2);
     issue_rows(s + lead, islot, NPW / 2, 3 * NPW / 4);
     bool resc;
-    const float alpha = softmax(NoMaskT{}, s, sc, pw_prev, resc);
+    const float alpha = softmax(NoMaskT{}, s, sc, pw_prev, resc, &sc_max);
     issue_rows(s + lead, islot, 3 * NPW / 4, NPW);
     if (resc) rescale(alpha);
     sc = nxt;
+    sc_max = row_max(nxt);
   };
   // unrolled by SL from s = 1 (mod SL): every slot is a constant (the
   // addresses fold) and the next-step scores take turns in registers
+  if (s < n_hot) sc_max = row_max(sc);
   for (; s + SL <= n_hot; s += SL) {
 #pragma unroll
     for (int u = 0; u < SL; ++u) hot(s + u, (u + 2) % SL, u % SL, isk ? (u + 1) % SL : (u + SL - 1) % SL);
