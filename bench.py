@@ -17,7 +17,8 @@ value = 2^40 algorithmic FLOP per step / wall time per step (TFLOP/s).
 The other BASELINE configs (attention prefill, residual+RMSNorm, masked
 softmax, int8 decode, RMSNorm->MatMul) are reported under "extra", each with
 the CPU oracle timed on one thread and on all threads (a bounded sample,
-extrapolated per row / head where it is smaller than the workload) and the
+extrapolated per row / head where it is smaller than the workload, repeated
+until ~10 s of CPU time per leg) and the
 parity of the GPU output on that sample; the config-2 oracle timing is
 "cpu_baseline".  One JSON line is printed.
 
@@ -204,13 +205,17 @@ def host_info() -> dict:
     return {"nproc": usable, "cpu_model": model}
 
 
+CPU_LEG_SECONDS = 10.0  # CPU work per baseline leg: the sample is run again until this much time has passed
+
+
 def cpu_pair(run, single_sample, all_sample, unit: str, work_per_unit: float, total_units: float,
-             what: str) -> dict:
+             what: str, leg_seconds: float = CPU_LEG_SECONDS) -> dict:
     """Time the oracle (the C restatement of kernels/cpu) on one thread and on
     every thread OpenMP gives it: run(sample) processes `sample` units (rows,
     queries, ...) of the workload, `work_per_unit` is the metric's work (FLOP
     or algorithmic bytes) per unit, extrapolated to `total_units` when the
-    sample is smaller than the workload."""
+    sample is smaller than the workload.  Each leg repeats its sample until
+    `leg_seconds` of CPU time have passed (at least once)."""
     from oracle import pyoracle
 
     threads = pyoracle.num_threads()
@@ -220,14 +225,19 @@ def cpu_pair(run, single_sample, all_sample, unit: str, work_per_unit: float, to
         try:
             t0 = time.perf_counter()
             out = run(sample)
+            reps = 1
+            while time.perf_counter() - t0 < leg_seconds:
+                run(sample)
+                reps += 1
             dt = time.perf_counter() - t0
         finally:
             pyoracle.set_num_threads(threads)
         scale = 1e12 if unit == "TFLOP/s" else 1e9
-        res[name] = {"value": round(sample * work_per_unit / dt / scale, 6), "unit": unit, "cores": nthr,
-                     "kind": "port", "seconds": round(dt, 3),
+        res[name] = {"value": round(reps * sample * work_per_unit / dt / scale, 6), "unit": unit, "cores": nthr,
+                     "kind": "port", "seconds": round(dt, 3), "repetitions": reps,
                      "sample": f"{sample:g} of {total_units:g} {what}" +
-                               (" (extrapolated per unit)" if sample < total_units else " (full workload)")}
+                               (" (extrapolated per unit)" if sample < total_units else " (full workload)") +
+                               f", run {reps} times"}
         res.setdefault("_outputs", {})[name] = out
     return res
 
