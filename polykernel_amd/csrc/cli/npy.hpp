@@ -72,6 +72,7 @@ inline std::vector<int64_t> Shape(const std::string &h) {
     const size_t start = i;
     while (i < close && h[i] >= '0' && h[i] <= '9') ++i;
     if (i == start) throw Error("npy header: non-integer dimension in 'shape'");
+    if (i - start > 15) throw Error("npy header: dimension " + h.substr(start, i - start) + " is too large");
     shape.push_back(std::stoll(h.substr(start, i - start)));
   }
   return shape;
@@ -128,9 +129,23 @@ inline Array Read(const std::string &path, const std::vector<std::string> &want 
     if (!ok) throw Error(path + ": dtype '" + a.descr + "' where " + want[0] + " was expected");
   }
   a.shape = detail::Shape(h);
-  for (int64_t d : a.shape)
+  // the payload's size, checked for overflow, against what the file holds
+  // before anything is allocated
+  uint64_t bytes = (uint64_t)isz;
+  for (int64_t d : a.shape) {
     if (d < 0) throw Error(path + ": negative dimension");
-  a.data.resize((size_t)a.size() * isz);
+    if (d != 0 && bytes > (uint64_t(1) << 62) / (uint64_t)d)
+      throw Error(path + ": shape " + detail::ShapeRepr(a.shape) + " is too large");
+    bytes *= (uint64_t)d;
+  }
+  const std::streampos here = in.tellg();
+  in.seekg(0, std::ios::end);
+  const std::streampos end = in.tellg();
+  in.seekg(here);
+  if (!in || here < 0 || end < here || (uint64_t)(end - here) < bytes)
+    throw Error(path + ": truncated .npy payload (shape " + detail::ShapeRepr(a.shape) + " needs " + std::to_string(bytes) +
+                " bytes)");
+  a.data.resize((size_t)bytes);
   in.read(reinterpret_cast<char *>(a.data.data()), (std::streamsize)a.data.size());
   if (!in) throw Error(path + ": truncated .npy payload");
   return a;

@@ -76,3 +76,22 @@ def test_bad_inputs_are_errors(tmp_path):
     assert run("matmul", "a.npy").returncode == 2          # wrong arity: usage
     assert run("frobnicate").returncode == 2               # unknown op
     assert run("softmax", "a", "b", "--nope", "1").returncode == 2
+
+
+def _npy_with_header(path, header: str, payload: bytes = bytes(16)):
+    h = header.encode()
+    h = h + b" " * (64 - (10 + len(h) + 1) % 64) + b"\n"
+    path.write_bytes(b"\x93NUMPY\x01\x00" + len(h).to_bytes(2, "little") + h + payload)
+
+
+@pytest.mark.parametrize("shape,msg", [("(99999999999999999999,)", "is too large"),
+                                       ("(4000000000, 4000000000, 4000000000)", "is too large"),
+                                       ("(400000000000, 4)", "truncated .npy payload"),
+                                       ("(5, 4)", "truncated .npy payload")])
+def test_oversized_or_truncated_payload_is_refused_before_allocating(tmp_path, shape, msg):
+    """A header whose shape overflows, or declares more bytes than the file
+    holds, is an error with a message; nothing is allocated for it."""
+    f = tmp_path / "bad.npy"
+    _npy_with_header(f, "{'descr': '<f4', 'fortran_order': False, 'shape': %s, }" % shape)
+    r = run("roundtrip", f, tmp_path / "out.npy")
+    assert r.returncode == 1 and msg in r.stderr, r.stderr
