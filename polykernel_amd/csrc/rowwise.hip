@@ -54,7 +54,7 @@ int rmsnorm_dispatch(const uint16_t *x, const uint16_t *r, const uint16_t *w, ui
   const int nvec = cols / 8;
   if (vec && nvec <= 64 * 8) {
     // one wave per row, 4 rows per block
-    const dim3 grid((rows + 3) / 4);
+    const dim3 grid(rows / 4 + (rows % 4 != 0));
 #define PK_RMS_W(VPT) rmsnorm_vec_kernel<1, VPT, RESID><<<grid, kBlock, 0, st>>>(a)
     if (nvec <= 64) PK_RMS_W(1);
     else if (nvec <= 128) PK_RMS_W(2);
@@ -94,7 +94,7 @@ int softmax_dispatch(const void *in, const uint16_t *mask, uint16_t *y, int rows
   const bool vec = (cols % 8 == 0) && aligned16(in) && aligned16(y) && (MODE == 0 || aligned16(mask));
   const int nvec = cols / 8;
   if (vec && nvec <= 64 * 4) {
-    const dim3 grid((rows + 3) / 4);
+    const dim3 grid(rows / 4 + (rows % 4 != 0));
 #define PK_SM_W(VPT) softmax_vec_kernel<1, VPT, MODE><<<grid, kBlock, 0, st>>>(a)
     if (nvec <= 64) PK_SM_W(1);
     else if (nvec <= 128) PK_SM_W(2);

@@ -101,9 +101,9 @@ __device__ __forceinline__ void rmsnorm_vec_body(const RowArgs &a) {
   __shared__ float red[NW];
   constexpr int kRowsPerBlock = (NW == 1) ? (kBlock / 64) : 1;
   constexpr int kLanes = NW * 64;
-  const int row = (NW == 1) ? (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) : blockIdx.x;
+  const unsigned row = (NW == 1) ? (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) : blockIdx.x;
   const int lane = (NW == 1) ? (threadIdx.x & 63) : threadIdx.x;
-  if (row >= rows) return;  // uniform per row-group (NW == 1: per wave)
+  if (row >= (unsigned)rows) return;  // uniform per row-group (NW == 1: per wave)
   const int nvec = cols >> 3;
   const size_t base = (size_t)row * cols;
 
@@ -242,9 +242,9 @@ __device__ __forceinline__ void softmax_vec_body(const RowArgs &a) {
   __shared__ float red[NW];
   constexpr int kRowsPerBlock = (NW == 1) ? (kBlock / 64) : 1;
   constexpr int kLanes = NW * 64;
-  const int row = (NW == 1) ? (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) : blockIdx.x;
+  const unsigned row = (NW == 1) ? (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) : blockIdx.x;
   const int lane = (NW == 1) ? (threadIdx.x & 63) : threadIdx.x;
-  if (row >= rows) return;
+  if (row >= (unsigned)rows) return;
   const int nvec = cols >> 3;
   const size_t base = (size_t)row * cols;
 

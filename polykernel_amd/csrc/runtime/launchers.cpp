@@ -260,7 +260,7 @@ std::optional<CachedBinary> BinaryOf(const ModuleTable &table, const CacheEntry 
 bool RowLaunch(ModuleTable::Loaded *mod, const Config &c, pk_row_args a, void *stream, std::string &error) {
   const bool vec = c.vector_width == 8 && a.cols % 8 == 0 && Aligned16(a.in) && Aligned16(a.out) &&
                    (!a.aux || Aligned16(a.aux)) && (!a.gamma || Aligned16(a.gamma));
-  const unsigned grid = vec && c.block_m == 4 ? (unsigned)((a.rows + 3) / 4) : (unsigned)a.rows;
+  const unsigned grid = vec && c.block_m == 4 ? (unsigned)(a.rows / 4 + (a.rows % 4 != 0)) : (unsigned)a.rows;
   return ModuleLaunch(mod->fns[vec ? 0 : 1], grid, 1, 256, stream, a, vec ? "pk_row" : "pk_row_any", error);
 }
 
