@@ -202,7 +202,7 @@ __global__ __launch_bounds__(I8_THREADS) void int8_gemm_kernel(Int8Args g) {
 // loaded with 16-byte loads (independent, so they are all in flight at once)
 // and added in split order.  Needs N % 8 == 0 and 16-byte aligned buffers.
 template <int EPI>
-__global__ __launch_bounds__(256) void int8_reduce8_kernel(Int8Args g) {
+__global__ __launch_bounds__(PK_I8_REDUCE_THREADS) void int8_reduce8_kernel(Int8Args g) {
   reduce8_body<EPI>(g.partial, g.splits, g.M, g.N, g.scale, g.R, g.gelu_tab, g.C);
 }
 
@@ -483,10 +483,11 @@ int int8_run(int epi, const uint16_t *A, const int8_t *W, const float *scale, ui
     const bool vec = N % 8 == 0 && aligned16(g.partial) && aligned16(scale) && aligned16(C) &&
                      (epi != I8_RESID || aligned16(R));
     if (vec) {
-      const int blocks = (int)std::min<int64_t>((total / 8 + 255) / 256, 4096);
-      if (epi == I8_NONE) int8_reduce8_kernel<I8_NONE><<<blocks, 256, 0, st>>>(g);
-      else if (epi == I8_GELU) int8_reduce8_kernel<I8_GELU><<<blocks, 256, 0, st>>>(g);
-      else int8_reduce8_kernel<I8_RESID><<<blocks, 256, 0, st>>>(g);
+      constexpr int T = PK_I8_REDUCE_THREADS;
+      const int blocks = (int)std::min<int64_t>((total / 8 + T - 1) / T, 4096);
+      if (epi == I8_NONE) int8_reduce8_kernel<I8_NONE><<<blocks, T, 0, st>>>(g);
+      else if (epi == I8_GELU) int8_reduce8_kernel<I8_GELU><<<blocks, T, 0, st>>>(g);
+      else int8_reduce8_kernel<I8_RESID><<<blocks, T, 0, st>>>(g);
     } else {
       const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
       if (epi == I8_NONE) int8_reduce_kernel<I8_NONE><<<blocks, 256, 0, st>>>(g);

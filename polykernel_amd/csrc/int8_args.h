@@ -20,4 +20,8 @@ typedef struct pk_i8s_args {
   int units;        /* column slices * splits */
 } pk_i8s_args;
 
+/* Threads per workgroup of the split reduction (reduce8_body), for every host
+ * that launches it: 8 outputs per thread, one grid-stride pass. */
+#define PK_I8_REDUCE_THREADS 128
+
 #endif /* PK_INT8_ARGS_H */

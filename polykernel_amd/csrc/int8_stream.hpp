@@ -24,15 +24,12 @@ typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
 
 
-// Epilogue of 8 consecutive outputs (m, n..n+7) from their fp32 dot products:
-// scale, bf16, then GELU or residual add, one 16-byte store.  Needs n % 8 == 0
-// and 16-byte aligned scale, C and R rows.
+// Epilogue of 8 consecutive outputs from their fp32 dot products v0, v1 and
+// the matching scales sc0, sc1 (and residual words rv): scale, bf16, then GELU
+// or residual add, one 16-byte store to `out`.
 template <int EPI>
-__device__ __forceinline__ void int8_epilogue8(const f32x4 v0, const f32x4 v1, int m, int n, int N,
-                                               const float *scale, const uint16_t *R,
-                                               const uint16_t *gelu_tab, uint16_t *C) {
-  const f32x4 sc0 = *reinterpret_cast<const f32x4 *>(scale + n);
-  const f32x4 sc1 = *reinterpret_cast<const f32x4 *>(scale + n + 4);
+__device__ __forceinline__ void int8_finish8(const f32x4 v0, const f32x4 v1, const f32x4 sc0, const f32x4 sc1,
+                                             const u32x4 rv, const uint16_t *gelu_tab, uint16_t *out) {
   float y[8];
   {
 #pragma clang fp contract(off)
@@ -42,8 +39,6 @@ __device__ __forceinline__ void int8_epilogue8(const f32x4 v0, const f32x4 v1, i
       y[4 + e] = v1[e] * sc1[e];
     }
   }
-  u32x4 rv = {0, 0, 0, 0};
-  if constexpr (EPI == I8_RESID) rv = *reinterpret_cast<const u32x4 *>(R + (size_t)m * N + n);
   uint32_t o[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -57,29 +52,73 @@ __device__ __forceinline__ void int8_epilogue8(const f32x4 v0, const f32x4 v1, i
     }
     o[e] = t0 | (t1 << 16);
   }
-  *reinterpret_cast<u32x4 *>(C + (size_t)m * N + n) = u32x4{o[0], o[1], o[2], o[3]};
+  *reinterpret_cast<u32x4 *>(out) = u32x4{o[0], o[1], o[2], o[3]};
 }
 
-// Split reduction, 8 outputs per thread: the partials of all splits are
-// loaded with 16-byte loads (independent, so they are all in flight at once)
-// and added in split order.  Needs N % 8 == 0 and 16-byte aligned buffers.
+// The same for outputs (m, n..n+7) of a [M, N] result, loading the scales and
+// the residual.  Needs n % 8 == 0 and 16-byte aligned scale, C and R rows.
+template <int EPI>
+__device__ __forceinline__ void int8_epilogue8(const f32x4 v0, const f32x4 v1, int m, int n, int N,
+                                               const float *scale, const uint16_t *R,
+                                               const uint16_t *gelu_tab, uint16_t *C) {
+  const f32x4 sc0 = *reinterpret_cast<const f32x4 *>(scale + n);
+  const f32x4 sc1 = *reinterpret_cast<const f32x4 *>(scale + n + 4);
+  u32x4 rv = {0, 0, 0, 0};
+  if constexpr (EPI == I8_RESID) rv = *reinterpret_cast<const u32x4 *>(R + (size_t)m * N + n);
+  int8_finish8<EPI>(v0, v1, sc0, sc1, rv, gelu_tab, C + (size_t)m * N + n);
+}
+
+// Split reduction, 8 outputs per thread, PK_I8_REDUCE_THREADS threads per
+// workgroup: the partials of all splits are loaded with 16-byte loads
+// (independent, so they are all in flight at once) and added in split order.
+// A thread's first group issues every load it needs (partials, scales,
+// residual) before the workgroup copies the GELU table into LDS, so the
+// table's lookups wait for LDS rather than for a second round trip to memory.
+// Needs N % 8 == 0 and 16-byte aligned buffers.
 template <int EPI>
 __device__ __forceinline__ void reduce8_body(const float *partial, int splits, int M, int N, const float *scale,
                                              const uint16_t *R, const uint16_t *gelu_tab, uint16_t *C) {
   const int64_t total = (int64_t)M * N;
   const int64_t groups = total / 8;
-  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < groups; t += (int64_t)gridDim.x * 256) {
-    const int64_t e = 8 * t;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  __shared__ uint32_t tab_lds[EPI == I8_GELU ? (GELU_TABLE_SIZE + 1) / 2 : 1];
+  auto sum_splits = [&](int64_t e, f32x4 &s0, f32x4 &s1) __attribute__((always_inline)) {
     const float *p = partial + e;
-    f32x4 s0 = *reinterpret_cast<const f32x4 *>(p), s1 = *reinterpret_cast<const f32x4 *>(p + 4);
+    s0 = *reinterpret_cast<const f32x4 *>(p);
+    s1 = *reinterpret_cast<const f32x4 *>(p + 4);
 #pragma unroll 8
     for (int sp = 1; sp < splits; ++sp) {
       const float *q = p + (size_t)sp * total;
       s0 += *reinterpret_cast<const f32x4 *>(q);
       s1 += *reinterpret_cast<const f32x4 *>(q + 4);
     }
-    const int m = (int)(e / N), n = (int)(e % N);
-    int8_epilogue8<EPI>(s0, s1, m, n, N, scale, R, gelu_tab, C);
+  };
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, sc0 = s0, sc1 = s0;
+  u32x4 rv = {0, 0, 0, 0};
+  if (t0 < groups) {
+    const int64_t e = 8 * t0;
+    const int n = (int)(e % N);
+    sc0 = *reinterpret_cast<const f32x4 *>(scale + n);
+    sc1 = *reinterpret_cast<const f32x4 *>(scale + n + 4);
+    if constexpr (EPI == I8_RESID) rv = *reinterpret_cast<const u32x4 *>(R + e);
+    sum_splits(e, s0, s1);
+  }
+  const uint16_t *tab = gelu_tab;
+  if constexpr (EPI == I8_GELU) {
+    for (int i = threadIdx.x; i < (GELU_TABLE_SIZE + 1) / 2; i += blockDim.x)
+      tab_lds[i] = reinterpret_cast<const uint32_t *>(gelu_tab)[i];
+    __syncthreads();
+    tab = reinterpret_cast<const uint16_t *>(tab_lds);
+  }
+  if (t0 < groups) int8_finish8<EPI>(s0, s1, sc0, sc1, rv, tab, C + 8 * t0);
+  for (int64_t t = t0 + stride; t < groups; t += stride) {
+    const int64_t e = 8 * t;
+    const int n = (int)(e % N);
+    sum_splits(e, s0, s1);
+    if constexpr (EPI == I8_RESID) rv = *reinterpret_cast<const u32x4 *>(R + e);
+    int8_finish8<EPI>(s0, s1, *reinterpret_cast<const f32x4 *>(scale + n),
+                      *reinterpret_cast<const f32x4 *>(scale + n + 4), rv, tab, C + e);
   }
 }
 

@@ -14,7 +14,7 @@
 // Emitted entry points:
 //   matmul_int8, matmul_int8_gelu, matmul_int8_residual (int8_stream.hpp):
 //     pk_int8_stream(pk_i8s_args)  grid (slices * splits, m-blocks), 64 * num_warps threads
-//     pk_int8_reduce(pk_i8s_args)  the split reduction, 256 threads
+//     pk_int8_reduce(pk_i8s_args)  the split reduction, PK_I8_REDUCE_THREADS threads
 //   matmul, fused_matmul_bias_gelu, fused_matmul_bias_residual (gemm_kernels.hpp):
 //     pk_gemm(pk_gemm_args)        grid ceil(M/block_m) * ceil(N/block_n), 64 * num_warps threads;
 //                                  block_k 32: the DMA-ring kernel at shared_memory_stages,
@@ -284,7 +284,7 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
     << "extern \"C\" __global__ __launch_bounds__(" << 64 * c.num_warps << ", 1) void pk_int8_stream(pk_i8s_args g) {\n"
     << "  pk::i8s::stream_body<" << nt << ", " << mt << ", " << c.num_warps << ", " << c.shared_memory_stages << ", "
     << epi << ">(g);\n}\n\n"
-    << "extern \"C\" __global__ __launch_bounds__(256) void pk_int8_reduce(pk_i8s_args g) {\n"
+    << "extern \"C\" __global__ __launch_bounds__(PK_I8_REDUCE_THREADS) void pk_int8_reduce(pk_i8s_args g) {\n"
     << "  pk::i8s::reduce8_body<" << epi << ">(g.partial, g.splits, g.M, g.N, g.scale, g.R, g.gelu_tab, g.C);\n}\n";
   source = s.str();
   return true;

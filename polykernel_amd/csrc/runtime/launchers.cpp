@@ -190,8 +190,9 @@ LaunchFn CodeObjectInt8Launcher(int epi, std::shared_ptr<ModuleTable> table) {
       return false;
     if (splits > 1) {
       const long long groups = (long long)p->M * p->N / 8;
-      const unsigned blocks = (unsigned)std::min<long long>((groups + 255) / 256, 4096);
-      if (!ModuleLaunch(mod->fns[1], blocks, 1, 256, p->stream, a, "pk_int8_reduce", error)) return false;
+      constexpr long long T = PK_I8_REDUCE_THREADS;
+      const unsigned blocks = (unsigned)std::min<long long>((groups + T - 1) / T, 4096);
+      if (!ModuleLaunch(mod->fns[1], blocks, 1, (unsigned)T, p->stream, a, "pk_int8_reduce", error)) return false;
     }
     return true;
   };
