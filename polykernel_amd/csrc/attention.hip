@@ -85,12 +85,22 @@ int pick_splits(int BH, int q_tiles, int kv_tiles) {
   return s;
 }
 
+// The kernels split blockIdx.x into (bh, query tile, key split) in 32-bit
+// arithmetic: the grid must stay within INT32_MAX workgroups.
+int grid_ok(int64_t BH, int64_t q_tiles, int64_t splits, const char *name) {
+  if (BH * q_tiles * splits <= INT32_MAX) return PK_OK;
+  set_error("%s: %lld (b,h) x %lld query tiles x %lld key splits exceeds %d workgroups", name, (long long)BH,
+            (long long)q_tiles, (long long)splits, INT32_MAX);
+  return PK_ERR_UNSUPPORTED;
+}
+
 template <int DP>
 int attention_dp(AttArgs g, hipStream_t st, const AttModule *mod) {
   const bool aligned = (g.D % 8 == 0) && aligned16(g.Q) && aligned16(g.K) && aligned16(g.V);
   g.q_tiles = (g.S_q + AT_BQ - 1) / AT_BQ;
   const int kv_tiles = (g.S_kv + AT_BKV - 1) / AT_BKV;
   g.splits = pick_splits(g.BH, g.q_tiles, kv_tiles);
+  if (int rc = grid_ok(g.BH, g.q_tiles, g.splits, "attention")) return rc;
   WorkspaceLease lease;  // held until the combine kernel is queued
   if (g.splits > 1) {
     const size_t rows = (size_t)g.BH * g.S_q;
@@ -127,6 +137,7 @@ int attention_wide(AttArgs g, hipStream_t st, const AttModule *mod) {
   g.q_tiles = (g.S_q + AW_BQ - 1) / AW_BQ;
   const int kv_tiles = (g.S_kv + AW_BKV - 1) / AW_BKV;
   g.splits = pick_splits(g.BH, g.q_tiles, kv_tiles);
+  if (int rc = grid_ok(g.BH, g.q_tiles, g.splits, "attention")) return rc;
   WorkspaceLease lease;  // held until the combine kernel is queued
   if (g.splits > 1) {
     const size_t rows = (size_t)g.BH * g.S_q;
@@ -211,6 +222,7 @@ int attention_fa(FaArgs a, int D, int qg, hipStream_t st, const AttModule *mod) 
   const int ntiles = (a.S_kv + BKV - 1) / BKV;
   a.splits = 1;
   while ((int64_t)a.BH * a.q_tiles * a.splits < 256 && ntiles / (2 * a.splits) >= 8 && a.splits < 8) a.splits *= 2;
+  if (int rc = grid_ok(a.BH, a.q_tiles, a.splits, "attention")) return rc;
   WorkspaceLease lease;  // held until the merge kernel is queued
   if (a.splits > 1) {
     const size_t rows = (size_t)a.BH * a.S_q;
@@ -347,6 +359,10 @@ int fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc, con
                "launch_fused_kv_append_attention: null tensor pointer");
   PK_CHECK_ARG(B >= 0 && H >= 0 && S_q >= 0 && S_cache >= 0 && D > 0,
                "launch_fused_kv_append_attention: invalid shape");
+  PK_CHECK_ARG(cache_capacity <= INT32_MAX - 1023,
+               "launch_fused_kv_append_attention: cache_capacity %d is within 1023 of INT32_MAX (the kernels round "
+               "key counts up to whole tiles in 32-bit arithmetic)",
+               cache_capacity);
   PK_CHECK_ARG((int64_t)S_cache + S_q <= cache_capacity,
                "launch_fused_kv_append_attention: S_cache + S_q = %lld exceeds cache_capacity %d",
                (long long)S_cache + S_q, cache_capacity);
@@ -356,8 +372,10 @@ int fused_kv_append_attention(const uint16_t *Q, uint16_t *Kc, uint16_t *Vc, con
   }
   const int64_t BH = (int64_t)B * H;
   if (BH == 0) return PK_OK;
+  PK_CHECK_ARG(BH <= INT32_MAX, "launch_fused_kv_append_attention: B * H = %lld exceeds %d", (long long)BH,
+               INT32_MAX);
   const int S_kv = S_cache + S_q;
-  if (S_q > 0 && BH <= INT32_MAX && scale > 0.f && mode >= 0) {
+  if (S_q > 0 && scale > 0.f && mode >= 0) {
     int qg = mode ? mode : fa_default_qg(BH, S_q);
     auto fits = [&](int g) {
       return fa_applicable(S_kv, S_cache, D, cache_capacity, Q, Kc, Vc, O, Kn, Vn, Kc, Vc, fa_bkv(g));
@@ -396,7 +414,13 @@ int launch_attention_prefill(const uint16_t *Q, const uint16_t *K, const uint16_
   PK_CHECK_ARG(Q && K && V && O, "launch_attention_prefill: null tensor pointer");
   PK_CHECK_ARG(B >= 0 && H >= 0 && S_q >= 0 && S_kv >= 0 && D > 0,
                "launch_attention_prefill: invalid shape");
+  PK_CHECK_ARG(S_q <= INT32_MAX - 1023 && S_kv <= INT32_MAX - 1023,
+               "launch_attention_prefill: S_q = %d or S_kv = %d is within 1023 of INT32_MAX (the kernels round "
+               "them up to whole tiles in 32-bit arithmetic)",
+               S_q, S_kv);
   if ((int64_t)B * H * S_q == 0) return PK_OK;
+  PK_CHECK_ARG((int64_t)B * H <= INT32_MAX, "launch_attention_prefill: B * H = %lld exceeds %d",
+               (long long)B * H, INT32_MAX);
   return attention_run(Q, K, V, O, B * H, S_q, S_kv, D, S_kv, scale, causal, 0, (hipStream_t)stream);
 }
 

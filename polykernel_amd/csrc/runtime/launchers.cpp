@@ -128,6 +128,25 @@ bool ModuleLaunch(void *fn, unsigned gx, unsigned gy, unsigned threads, void *st
   return true;
 }
 
+// Workgroups of an output tiling of [M, N] by bm x bn tiles; the kernels
+// round M and N up to tiles and decode blockIdx.x in 32-bit arithmetic, so
+// M or N within 1023 of INT32_MAX, or more than INT32_MAX tiles, is an error.
+bool TileGrid(int M, int N, int bm, int bn, unsigned &tiles, std::string &error) {
+  if (bm <= 0 || bn <= 0 || M > INT32_MAX - 1023 || N > INT32_MAX - 1023) {
+    error = "output tiling of " + std::to_string(M) + " x " + std::to_string(N) + " by " + std::to_string(bm) +
+            " x " + std::to_string(bn) + ": tiles must be positive and M, N at least 1023 below INT32_MAX";
+    return false;
+  }
+  const long long t = (((long long)M + bm - 1) / bm) * (((long long)N + bn - 1) / bn);
+  if (t > INT32_MAX) {
+    error = "output tiling of " + std::to_string(M) + " x " + std::to_string(N) + " by " + std::to_string(bm) +
+            " x " + std::to_string(bn) + " needs more than INT32_MAX workgroups";
+    return false;
+  }
+  tiles = (unsigned)t;
+  return true;
+}
+
 // The launch geometry of an int8 config follows from its fields: column
 // slices of block_n, K splits of block_k rows (64-row steps), row blocks of
 // block_m; the streaming kernel and, with more than one split, the split
@@ -240,7 +259,8 @@ LaunchFn CodeObjectGemmLauncher(int epi, std::shared_ptr<ModuleTable> table) {
       return false;
     }
     pk_gemm_args a{p->A, p->B, p->C, bias, R, tab, p->M, p->N, p->K};
-    const unsigned tiles = (unsigned)(((p->M + c.block_m - 1) / c.block_m) * ((p->N + c.block_n - 1) / c.block_n));
+    unsigned tiles = 0;
+    if (!TileGrid(p->M, p->N, c.block_m, c.block_n, tiles, error)) return false;
     return ModuleLaunch(mod->fns[0], tiles, 1, 64u * c.num_warps, p->stream, a, "pk_gemm", error);
   };
 }
@@ -327,7 +347,8 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
       ModuleTable::Loaded *mod = table->Get(*bin, {"pk_panel"}, error);
       if (!mod) return false;
       pk_panel_args a{p->x, p->gamma, p->W, p->out, p->M, p->N, p->K, 1.0f / (float)p->K, p->eps};
-      const unsigned tiles = (unsigned)(((p->M + 31) / 32) * ((p->N + 63) / 64));
+      unsigned tiles = 0;
+      if (!TileGrid(p->M, p->N, 32, 64, tiles, error)) return false;
       const unsigned lds = fast ? (unsigned)(p->K * 128 + 32 * p->K * 2) : (unsigned)(32 * p->K * 2 + 2 * 64 * 64 * 2);
       return ModuleLaunch(mod->fns[0], tiles, 1, fast ? 256u : 128u, p->stream, a, "pk_panel", error, lds);
     }
@@ -362,7 +383,8 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
                    p->stream, error))
       return false;
     pk_gemm_args g{xn, p->W, p->out, nullptr, nullptr, nullptr, p->M, p->N, p->K};
-    const unsigned tiles = (unsigned)(((p->M + c.block_m - 1) / c.block_m) * ((p->N + c.block_n - 1) / c.block_n));
+    unsigned tiles = 0;
+    if (!TileGrid(p->M, p->N, c.block_m, c.block_n, tiles, error)) return false;
     return ModuleLaunch(mod->fns[2], tiles, 1, 64u * c.num_warps, p->stream, g, "pk_gemm", error);
   };
 }

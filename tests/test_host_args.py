@@ -80,3 +80,53 @@ def test_int8_zero_k_is_an_error_not_a_crash():
     assert b"no configuration" in lib.pk_last_error()
     lib.pk_decode_mlp_int8_workspace_size.restype = C.c_size_t
     assert lib.pk_decode_mlp_int8_workspace_size(1, 0, 64) == 0
+
+
+_GRID_CHILD = r"""
+import ctypes as C, sys
+sys.path.insert(0, sys.argv[1])
+from polykernel_amd import _lib
+lib = _lib.load()
+P, I, F = C.c_void_p, C.c_int, C.c_float
+fake = P(0x100000)  # never dereferenced: every case is refused before a device call
+cases = [
+    # B * H above INT32_MAX
+    ("prefill", (65536, 65536, 1, 1, 128), "exceeds"),
+    # (b,h) x query tiles above INT32_MAX workgroups: generic kernel (D 96), wide kernel (D 512), flash (D 128)
+    # (128-query tiles: 2^21 x 2^10; 32-query tiles: 2^22 x 2^10; flash 128 x 64 tiles: 2^23 x 2^9)
+    ("prefill", (1 << 21, 1, 1 << 17, 1 << 17, 96), "workgroups"),
+    ("prefill", (1 << 22, 1, 1 << 15, 1 << 15, 512), "workgroups"),
+    ("prefill", (1 << 23, 1, 1 << 16, 64, 128), "workgroups"),
+    ("fused", (65536, 65536, 1, 0, 128), "exceeds"),
+    # output tilings above INT32_MAX workgroups: GEMM (64 x 64 smallest tile) and RMSNorm -> MatMul (32 x 64)
+    ("matmul", (2**31 - 1024, 2**31 - 1024, 64, 0, 0), "workgroups"),
+    ("rmsnorm_matmul", (2**31 - 1, 2**30, 64, 0, 0), "INT32_MAX"),
+    ("rmsnorm_matmul", (2**31 - 1024, 2**30, 64, 0, 0), "workgroups"),
+    # a dimension that rounds up past INT32_MAX
+    ("matmul", (2**31 - 1, 8, 32, 0, 0), "INT32_MAX"),
+    ("prefill", (1, 1, 2**31 - 1, 16, 64), "INT32_MAX"),
+    ("fused", (1, 1, 16, 2**31 - 20, 64), "INT32_MAX"),
+]
+for kind, (B, H, Sq, Skv, D), word in cases:
+    if kind == "prefill":
+        rc = lib.launch_attention_prefill(fake, fake, fake, fake, B, H, Sq, Skv, D, F(0.1), 1, None)
+    elif kind == "matmul":
+        rc = lib.launch_matmul(fake, fake, fake, B, H, Sq, None)
+    elif kind == "rmsnorm_matmul":
+        rc = lib.launch_fused_rmsnorm_matmul(fake, fake, fake, B, H, Sq, F(1e-6), None)
+    else:
+        rc = lib.launch_fused_kv_append_attention(fake, fake, fake, fake, fake, fake, B, H, Sq, Skv, D, Sq + Skv,
+                                                  F(0.1), 1, None)
+    msg = _lib.last_error()
+    assert rc < 0 and word in msg, (kind, B, H, Sq, Skv, D, rc, msg)
+print("ok")
+"""
+
+
+def test_grid_limits_are_refused_before_launch():
+    """Shapes whose grid would overflow the kernels' 32-bit workgroup index
+    (attention: B * H, or (b,h) x query tiles x key splits; GEMMs: output
+    tiles, above INT32_MAX) return an error before any device call."""
+    res = subprocess.run([sys.executable, "-c", _GRID_CHILD, str(ROOT)], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), \
+        f"child exited {res.returncode}:\n{res.stdout[-2000:]}\n{res.stderr[-2000:]}"
