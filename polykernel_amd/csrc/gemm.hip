@@ -53,12 +53,12 @@ int launch_tile(const GemmArgs &g, bool aligned, hipStream_t st) {
   return PK_OK;
 }
 
-// The kernels map blockIdx.x to (tile row, tile column) and round M and N up
-// to whole tiles in 32-bit arithmetic: M and N stay 1023 below INT32_MAX, and
-// a grid of the smallest tile (bm x bn) within INT32_MAX workgroups.
-int tile_grid_ok(int M, int N, int bm, int bn, const char *name) {
-  if (M > INT32_MAX - 1023 || N > INT32_MAX - 1023) {
-    set_error("%s: M=%d or N=%d is within 1023 of INT32_MAX", name, M, N);
+// The kernels map blockIdx.x to (tile row, tile column) and round M, N and K
+// up to whole tiles in 32-bit arithmetic: each stays 1023 below INT32_MAX,
+// and a grid of the smallest tile (bm x bn) within INT32_MAX workgroups.
+int tile_grid_ok(int M, int N, int K, int bm, int bn, const char *name) {
+  if (M > INT32_MAX - 1023 || N > INT32_MAX - 1023 || K > INT32_MAX - 1023) {
+    set_error("%s: M=%d, N=%d or K=%d is within 1023 of INT32_MAX", name, M, N, K);
     return PK_ERR_UNSUPPORTED;
   }
   if ((((int64_t)M + bm - 1) / bm) * (((int64_t)N + bn - 1) / bn) <= INT32_MAX) return PK_OK;
@@ -171,7 +171,7 @@ bool gemm_default(int M, int N, int K, pk_config *out) {
 
 int gemm_run_config(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
                     const uint16_t *R, int M, int N, int K, const pk_config &req, hipStream_t st) {
-  if (int rc = tile_grid_ok(M, N, 64, 64, "matmul")) return rc;
+  if (int rc = tile_grid_ok(M, N, K, 64, 64, "matmul")) return rc;
   GemmArgs g{A, B, C, bias, R, nullptr, M, N, K};
   const bool shape_vec = (K % 8 == 0) && (N % 8 == 0);
   const bool ptr_vec = aligned16(A) && aligned16(B);
@@ -211,7 +211,7 @@ int gemm_run_config(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, 
 
 int gemm_run(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const uint16_t *bias,
              const uint16_t *R, int M, int N, int K, hipStream_t st, int tile = -1) {
-  if (int rc = tile_grid_ok(M, N, 64, 64, "matmul")) return rc;
+  if (int rc = tile_grid_ok(M, N, K, 64, 64, "matmul")) return rc;
   GemmArgs g{A, B, C, bias, R, nullptr, M, N, K};
   if (epi == EPI_BIAS_GELU) {
     int rc = gelu_table(&g.gelu_tab);
@@ -261,7 +261,7 @@ int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_
   PK_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "%s: invalid shape M=%d N=%d K=%d", name, M, N, K);
   if (M == 0 || N == 0) return PK_OK;
   static_assert(RQ_BM == RP_BM && RQ_BN == RP_BN, "both panel kernels use 32 x 64 output tiles");
-  if (int rc = tile_grid_ok(M, N, RP_BM, RP_BN, name)) return rc;
+  if (int rc = tile_grid_ok(M, N, K, RP_BM, RP_BN, name)) return rc;
   const bool panel_ok = (K % BK == 0) && K <= RP_MAX_K && (N % 8 == 0) && aligned16(x) &&
                         aligned16(W) && (!gamma || aligned16(gamma));
   if (panel_ok && K <= RQ_MAX_K && aligned16(out) && (size_t)K * N * 2 < (size_t(1) << 31)) {
@@ -348,7 +348,7 @@ int launch_mlp_block(const uint16_t *x, const uint16_t *gamma, const uint16_t *W
   PK_CHECK_ARG(x && W1 && b1 && W2 && b2 && out, "launch_mlp_block: null tensor pointer");
   PK_CHECK_ARG(M >= 0 && d > 0 && F > 0, "launch_mlp_block: invalid shape");
   if (M == 0) return PK_OK;
-  if (int rc = tile_grid_ok(M, std::max(d, F), 64, 64, "launch_mlp_block")) return rc;  // before any launch
+  if (int rc = tile_grid_ok(M, std::max(d, F), std::max(d, F), 64, 64, "launch_mlp_block")) return rc;  // before any launch
   const size_t need = pk_mlp_block_workspace_size(M, d, F);
   if (!workspace || workspace_bytes < need) {
     set_error("launch_mlp_block: workspace of %zu bytes required, got %zu", need, workspace_bytes);

@@ -183,10 +183,12 @@ __global__ __launch_bounds__(kBlock) void quant_amax_kernel(const uint16_t *__re
                                                             int N) {
   const int n = blockIdx.x * kBlock + threadIdx.x;
   if (n >= N) return;
-  const int k0 = blockIdx.y * kQuantRows;
-  const int k1 = min(K, k0 + kQuantRows);
   uint32_t m = 0;
-  for (int k = k0; k < k1; ++k) m = max(m, (uint32_t)W[(size_t)k * N + n] & 0x7FFFu);
+  // chunks of kQuantRows rows, strided by the grid's y extent (at most 65535)
+  for (int64_t k0 = (int64_t)blockIdx.y * kQuantRows; k0 < K; k0 += (int64_t)gridDim.y * kQuantRows) {
+    const int64_t k1 = min((int64_t)K, k0 + kQuantRows);
+    for (int64_t k = k0; k < k1; ++k) m = max(m, (uint32_t)W[(size_t)k * N + n] & 0x7FFFu);
+  }
   // bf16 magnitude bits -> fp32 bits (exact upcast); max of non-negative floats.
   atomicMax(amax_bits + n, m << 16);
 }
@@ -324,11 +326,13 @@ int launch_quantize_int8_per_channel(const uint16_t *W, int8_t *Wq, float *scale
                                      void *stream) {
   PK_CHECK_ARG(W && Wq && scale, "launch_quantize_int8_per_channel: null tensor pointer");
   PK_CHECK_ARG(K > 0 && N > 0, "launch_quantize_int8_per_channel: invalid shape K=%d N=%d", K, N);
+  PK_CHECK_ARG(N <= INT32_MAX - kBlock, "launch_quantize_int8_per_channel: N=%d is within %d of INT32_MAX", N,
+               kBlock);
   hipStream_t st = (hipStream_t)stream;
   // The per-channel amax bits are staged in `scale` itself (same size, fp32).
   uint32_t *amax_bits = reinterpret_cast<uint32_t *>(scale);
   fill_u32_kernel<<<(N + kBlock - 1) / kBlock, kBlock, 0, st>>>(amax_bits, N, 0u);
-  dim3 g1((N + kBlock - 1) / kBlock, (K + kQuantRows - 1) / kQuantRows);
+  dim3 g1((N + kBlock - 1) / kBlock, (unsigned)std::min<int64_t>(((int64_t)K + kQuantRows - 1) / kQuantRows, 65535));
   quant_amax_kernel<<<g1, kBlock, 0, st>>>(W, amax_bits, K, N);
   quant_scale_kernel<<<(N + kBlock - 1) / kBlock, kBlock, 0, st>>>(amax_bits, scale, N);
   quant_apply_kernel<<<grid_for((int64_t)K * N), kBlock, 0, st>>>(W, scale, Wq, K, N);

@@ -171,7 +171,8 @@ __device__ __forceinline__ void rmsnorm_vec_body(const RowArgs &a) {
 }
 
 // Generic path (any cols / alignment): one block per row, two passes over the
-// row (the second from cache).
+// row (the second from cache).  Column indices are unsigned so that stepping
+// past a cols near INT32_MAX cannot wrap.
 template <bool RESID>
 __device__ __forceinline__ void rmsnorm_generic_body(const RowArgs &a) {
 #pragma clang fp contract(off)
@@ -185,14 +186,14 @@ __device__ __forceinline__ void rmsnorm_generic_body(const RowArgs &a) {
   const int row = blockIdx.x;
   const size_t base = (size_t)row * cols;
   float ss = 0.f;
-  for (int c = threadIdx.x; c < cols; c += kBlock) {
+  for (unsigned c = threadIdx.x; c < (unsigned)cols; c += kBlock) {
     float s = bf2f(x[base + c]);
     if constexpr (RESID) s = bf2f(f2bf(s + bf2f(r[base + c])));
     ss += s * s;
   }
   ss = group_sum<kBlock / 64>(ss, red);
   const float rms = sqrtf(ss * inv_cols + eps);
-  for (int c = threadIdx.x; c < cols; c += kBlock) {
+  for (unsigned c = threadIdx.x; c < (unsigned)cols; c += kBlock) {
     float s = bf2f(x[base + c]);
     if constexpr (RESID) s = bf2f(f2bf(s + bf2f(r[base + c])));
     float o = s / rms;
@@ -297,13 +298,13 @@ __device__ __forceinline__ void softmax_generic_body(const RowArgs &a) {
   const int row = blockIdx.x;
   const size_t base = (size_t)row * cols;
   float m = -INFINITY;
-  for (int c = threadIdx.x; c < cols; c += kBlock) m = fmaxf(m, load_z1<MODE>(in, mask, base + c));
+  for (unsigned c = threadIdx.x; c < (unsigned)cols; c += kBlock) m = fmaxf(m, load_z1<MODE>(in, mask, base + c));
   m = group_max<kBlock / 64>(m, red);
   float s = 0.f;
-  for (int c = threadIdx.x; c < cols; c += kBlock) s += expf(load_z1<MODE>(in, mask, base + c) - m);
+  for (unsigned c = threadIdx.x; c < (unsigned)cols; c += kBlock) s += expf(load_z1<MODE>(in, mask, base + c) - m);
   s = group_sum<kBlock / 64>(s, red);
   const float inv = 1.0f / s;
-  for (int c = threadIdx.x; c < cols; c += kBlock)
+  for (unsigned c = threadIdx.x; c < (unsigned)cols; c += kBlock)
     y[base + c] = (uint16_t)f2bf(expf(load_z1<MODE>(in, mask, base + c) - m) * inv);
 }
 

@@ -129,12 +129,13 @@ bool ModuleLaunch(void *fn, unsigned gx, unsigned gy, unsigned threads, void *st
 }
 
 // Workgroups of an output tiling of [M, N] by bm x bn tiles; the kernels
-// round M and N up to tiles and decode blockIdx.x in 32-bit arithmetic, so
-// M or N within 1023 of INT32_MAX, or more than INT32_MAX tiles, is an error.
-bool TileGrid(int M, int N, int bm, int bn, unsigned &tiles, std::string &error) {
-  if (bm <= 0 || bn <= 0 || M > INT32_MAX - 1023 || N > INT32_MAX - 1023) {
+// round M, N and K up to tiles and decode blockIdx.x in 32-bit arithmetic, so
+// a dimension within 1023 of INT32_MAX, or more than INT32_MAX tiles, is an
+// error.
+bool TileGrid(int M, int N, int K, int bm, int bn, unsigned &tiles, std::string &error) {
+  if (bm <= 0 || bn <= 0 || M > INT32_MAX - 1023 || N > INT32_MAX - 1023 || K > INT32_MAX - 1023) {
     error = "output tiling of " + std::to_string(M) + " x " + std::to_string(N) + " by " + std::to_string(bm) +
-            " x " + std::to_string(bn) + ": tiles must be positive and M, N at least 1023 below INT32_MAX";
+            " x " + std::to_string(bn) + ": tiles must be positive and M, N, K at least 1023 below INT32_MAX";
     return false;
   }
   const long long t = (((long long)M + bm - 1) / bm) * (((long long)N + bn - 1) / bn);
@@ -260,7 +261,7 @@ LaunchFn CodeObjectGemmLauncher(int epi, std::shared_ptr<ModuleTable> table) {
     }
     pk_gemm_args a{p->A, p->B, p->C, bias, R, tab, p->M, p->N, p->K};
     unsigned tiles = 0;
-    if (!TileGrid(p->M, p->N, c.block_m, c.block_n, tiles, error)) return false;
+    if (!TileGrid(p->M, p->N, p->K, c.block_m, c.block_n, tiles, error)) return false;
     return ModuleLaunch(mod->fns[0], tiles, 1, 64u * c.num_warps, p->stream, a, "pk_gemm", error);
   };
 }
@@ -348,7 +349,7 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
       if (!mod) return false;
       pk_panel_args a{p->x, p->gamma, p->W, p->out, p->M, p->N, p->K, 1.0f / (float)p->K, p->eps};
       unsigned tiles = 0;
-      if (!TileGrid(p->M, p->N, 32, 64, tiles, error)) return false;
+      if (!TileGrid(p->M, p->N, p->K, 32, 64, tiles, error)) return false;
       const unsigned lds = fast ? (unsigned)(p->K * 128 + 32 * p->K * 2) : (unsigned)(32 * p->K * 2 + 2 * 64 * 64 * 2);
       return ModuleLaunch(mod->fns[0], tiles, 1, fast ? 256u : 128u, p->stream, a, "pk_panel", error, lds);
     }
@@ -384,7 +385,7 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
       return false;
     pk_gemm_args g{xn, p->W, p->out, nullptr, nullptr, nullptr, p->M, p->N, p->K};
     unsigned tiles = 0;
-    if (!TileGrid(p->M, p->N, c.block_m, c.block_n, tiles, error)) return false;
+    if (!TileGrid(p->M, p->N, p->K, c.block_m, c.block_n, tiles, error)) return false;
     return ModuleLaunch(mod->fns[2], tiles, 1, 64u * c.num_warps, p->stream, g, "pk_gemm", error);
   };
 }

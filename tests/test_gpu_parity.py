@@ -199,6 +199,22 @@ def test_quantize_bit_exact(gpu, oracle, Kd, N):
     assert np.array_equal(from_dev(wq), owq)
 
 
+def test_quantize_rows_beyond_one_grid_pass(gpu, oracle):
+    """K above 65535 x 128 rows: the amax kernel's row chunks wrap around the
+    grid's y extent; a column whose largest magnitude sits only in the last
+    rows checks that those rows are reached."""
+    Kd, N = 65535 * 128 + 384, 8
+    _say(f"quantize K={Kd} N={N}")
+    w = synth.normal_bf16((Kd, N), 16, 1.0 / np.sqrt(Kd))
+    w[-1, 1] = bf([3.0])[0]
+    w[-200, 2] = bf([-5.0])[0]
+    wq, s = K().quantize_per_channel(to_dev(w))
+    owq, os_ = oracle.quantize_per_channel(w)
+    assert np.array_equal(from_dev(s).view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(from_dev(wq), owq)
+    assert from_dev(wq)[-1, 1] == 127 and from_dev(wq)[-200, 2] == -127
+
+
 def test_quantize_ties_bit_exact(gpu, oracle):
     col = np.array([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5], np.float32)
     w = bf(np.tile(col[:, None], (1, 16)))

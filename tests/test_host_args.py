@@ -104,6 +104,7 @@ cases = [
     ("rmsnorm_matmul", (2**31 - 1024, 2**30, 64, 0, 0), "workgroups"),
     # a dimension that rounds up past INT32_MAX
     ("matmul", (2**31 - 1, 8, 32, 0, 0), "INT32_MAX"),
+    ("matmul", (1, 8, 2**31 - 8, 0, 0), "INT32_MAX"),
     ("prefill", (1, 1, 2**31 - 1, 16, 64), "INT32_MAX"),
     ("fused", (1, 1, 16, 2**31 - 20, 64), "INT32_MAX"),
 ]
