@@ -270,6 +270,19 @@ PK_API int pk_fused_kv_append_attention_config(const uint16_t *Q, uint16_t *Kc, 
                                                int S_cache, int D, int cache_capacity, float scale, int causal,
                                                const pk_config *cfg, void *stream);
 
+/* launch_fused_residual_rmsnorm / launch_fused_softmax_mask with an explicit
+ * configuration (one of pk_op_configs("fused_residual_rmsnorm" or
+ * "fused_softmax_mask", rows, cols, 0); NULL = built-in choice), so the
+ * autotuner can time each row kernel variant (waves per row, vectors per
+ * lane).  A configuration not in the list returns PK_ERR_INVALID_ARG; a
+ * vector configuration (vector_width 8) with operands that are not 16-byte
+ * aligned returns PK_ERR_UNSUPPORTED. */
+PK_API int pk_fused_residual_rmsnorm_config(const uint16_t *x, const uint16_t *r, const uint16_t *gamma,
+                                            uint16_t *out, int rows, int cols, float eps, const pk_config *cfg,
+                                            void *stream);
+PK_API int pk_fused_softmax_mask_config(const float *logits, const uint16_t *mask, uint16_t *out, int rows,
+                                        int cols, const pk_config *cfg, void *stream);
+
 /* Negative launch probe: launches a trivial kernel with 2048 threads per
  * workgroup (twice the limit) and stores the hipError_t of the launch and of
  * the following synchronisation.  PK_OK when the invalid launch was caught

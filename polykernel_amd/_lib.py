@@ -79,6 +79,8 @@ SIGNATURES = {
     "launch_fused_matmul_bias_residual": (I, [P, P, P, P, P, I, I, I, P]),
     "launch_fused_kv_append_attention": (I, [P, P, P, P, P, P, I, I, I, I, I, I, F, I, P]),
     "pk_fused_kv_append_attention_config": (I, [P, P, P, P, P, P, I, I, I, I, I, I, F, I, C.POINTER(Config), P]),
+    "pk_fused_residual_rmsnorm_config": (I, [P, P, P, P, I, I, F, C.POINTER(Config), P]),
+    "pk_fused_softmax_mask_config": (I, [P, P, P, I, I, C.POINTER(Config), P]),
     "launch_quantize_int8_per_channel": (I, [P, P, P, I, I, P]),
     "pk_mlp_block_workspace_size": (SZ, [I, I, I]),
     "launch_mlp_block": (I, [P, P, P, P, P, P, P, I, I, I, F, P, SZ, P]),

@@ -376,8 +376,8 @@ int pk_op_configs(const char *op, long long M, long long N, long long K, pk_conf
     case OF_GEMM: return gemm_configs(m, n, k, out, cap);
     case OF_INT8: return int8_configs(m, n, k, out, cap);
     case OF_RMSNORM_MATMUL: return single(rmsnorm_matmul_config(m, n, k, &c), c, out, cap);
-    case OF_RMSNORM: return single(k == 0 && rmsnorm_config(m, n, &c), c, out, cap);
-    case OF_SOFTMAX: return single(k == 0 && softmax_config(m, n, &c), c, out, cap);
+    case OF_RMSNORM: return k == 0 ? rmsnorm_configs(m, n, out, cap) : 0;
+    case OF_SOFTMAX: return k == 0 ? softmax_configs(m, n, out, cap) : 0;
     case OF_ATTENTION: return n >= m ? attention_configs(m, n, k, out, cap) : 0;
     default: return 0;
   }

@@ -108,6 +108,8 @@ bool int8_default(int M, int N, int K, pk_config *out);
 bool rmsnorm_matmul_config(int M, int N, int K, pk_config *out);
 bool rmsnorm_config(int rows, int cols, pk_config *out);
 bool softmax_config(int rows, int cols, pk_config *out);
+int rmsnorm_configs(int rows, int cols, pk_config *out, int cap);
+int softmax_configs(int rows, int cols, pk_config *out, int cap);
 int attention_configs(int S_q, int S_kv, int D, pk_config *out, int cap);
 bool attention_config(int S_q, int S_kv, int D, pk_config *out);
 

@@ -1,6 +1,9 @@
 // rowwise.hip -- HBM-bound row kernels for gfx950: RMSNorm, residual+RMSNorm,
 // softmax, masked softmax (bodies in rowwise_kernels.hpp), GELU, KV append,
 // int8 per-channel quantisation, and their launchers.
+#include <algorithm>
+#include <cstring>
+
 #include "rowwise_kernels.hpp"
 
 namespace pk {
@@ -32,8 +35,10 @@ __global__ __launch_bounds__(kBlock) void div_check_kernel(const float *__restri
 }
 
 // The row kernels, as the library launches them (bodies in rowwise_kernels.hpp).
+// NW waves per row (NW == 1: one wave per row, 4 rows per 256-thread block;
+// otherwise one row per NW * 64-thread block), VPT 16-byte vectors per lane.
 template <int NW, int VPT, bool RESID>
-__global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(RowArgs a) {
+__global__ __launch_bounds__(NW > 4 ? NW * 64 : kBlock) void rmsnorm_vec_kernel(RowArgs a) {
   rmsnorm_vec_body<NW, VPT, RESID>(a);
 }
 
@@ -42,40 +47,8 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(RowArgs a) {
   rmsnorm_generic_body<RESID>(a);
 }
 
-template <bool RESID>
-int rmsnorm_dispatch(const uint16_t *x, const uint16_t *r, const uint16_t *w, uint16_t *y,
-                     int rows, int cols, float eps, hipStream_t st, const char *name) {
-  PK_CHECK_ARG(x && y && (!RESID || r), "%s: null tensor pointer", name);
-  PK_CHECK_ARG(rows >= 0 && cols > 0, "%s: invalid shape rows=%d cols=%d", name, rows, cols);
-  if (rows == 0) return PK_OK;
-  const RowArgs a{x, RESID ? r : nullptr, w, y, rows, cols, 1.0f / (float)cols, eps};
-  const bool vec = (cols % 8 == 0) && aligned16(x) && aligned16(y) && (!RESID || aligned16(r)) &&
-                   (!w || aligned16(w));
-  const int nvec = cols / 8;
-  if (vec && nvec <= 64 * 8) {
-    // one wave per row, 4 rows per block
-    const dim3 grid(rows / 4 + (rows % 4 != 0));
-#define PK_RMS_W(VPT) rmsnorm_vec_kernel<1, VPT, RESID><<<grid, kBlock, 0, st>>>(a)
-    if (nvec <= 64) PK_RMS_W(1);
-    else if (nvec <= 128) PK_RMS_W(2);
-    else if (nvec <= 256) PK_RMS_W(4);
-    else PK_RMS_W(8);
-#undef PK_RMS_W
-  } else if (vec && nvec <= 256 * 8) {
-    const dim3 grid(rows);
-#define PK_RMS_B(VPT) rmsnorm_vec_kernel<4, VPT, RESID><<<grid, kBlock, 0, st>>>(a)
-    if (nvec <= 256 * 4) PK_RMS_B(4);
-    else PK_RMS_B(8);
-#undef PK_RMS_B
-  } else {
-    rmsnorm_generic_kernel<RESID><<<rows, kBlock, 0, st>>>(a);
-  }
-  PK_LAUNCH_CHECK(name);
-  return PK_OK;
-}
-
 template <int NW, int VPT, int MODE>
-__global__ __launch_bounds__(kBlock) void softmax_vec_kernel(RowArgs a) {
+__global__ __launch_bounds__(NW > 4 ? NW * 64 : kBlock) void softmax_vec_kernel(RowArgs a) {
   softmax_vec_body<NW, VPT, MODE>(a);
 }
 
@@ -84,32 +57,176 @@ __global__ __launch_bounds__(kBlock) void softmax_generic_kernel(RowArgs a) {
   softmax_generic_body<MODE>(a);
 }
 
+// ---- configurations ---------------------------------------------------------
+// A row config: block_m = rows per workgroup (4: one wave per row; 1: one
+// row per workgroup of num_warps waves, 4 or 8), block_n = cols, num_warps,
+// vector_width = bf16 per load (8; 1 for the generic kernel, any cols and
+// alignment), unroll = 16-byte vectors per lane (the row stays in
+// registers), block_k 0 and stages 1.  Candidates, the built-in choice first:
+//   short rows (RMSNorm <= 512 vectors of 8, softmax <= 256): one wave per row;
+//   longer rows up to 2048 vectors: a workgroup per row at 4 and at 8 waves
+//   (8 first for softmax and for RMSNorm rows above 1024 vectors -- measured
+//   on [16384, 8192]: masked softmax 168.9 -> 162.0 us, residual+RMSNorm equal;
+//   at 16384 columns 174.2 -> 171.8 and 136.5 -> 128.0 us);
+//   cols % 8 != 0 or longer rows: the generic kernel.
+int row_vpt(int nvec, int lanes) {
+  for (int v : {1, 2, 4, 8})
+    if (lanes * v >= nvec) return v;
+  return 0;
+}
+
+int row_configs(bool softmax, int rows, int cols, pk_config *out, int cap) {
+  if (rows <= 0 || cols <= 0) return 0;
+  pk_config c[2];
+  int n = 0;
+  const int nvec = cols / 8;
+  if (cols % 8 == 0 && nvec <= (softmax ? 256 : 512)) {
+    c[n++] = pk_config{4, cols, 0, 4, 8, row_vpt(nvec, 64), 1};
+  } else if (cols % 8 == 0 && nvec <= 2048) {
+    // 4 waves: at least 4 vectors per lane for RMSNorm (the kernel's
+    // instantiations), 2 for softmax
+    const pk_config w4{1, cols, 0, 4, 8, std::max(softmax ? 2 : 4, row_vpt(nvec, 256)), 1};
+    const pk_config w8{1, cols, 0, 8, 8, std::max(softmax ? 1 : 2, row_vpt(nvec, 512)), 1};
+    const bool eight_first = softmax || nvec > 1024;
+    c[n++] = eight_first ? w8 : w4;
+    c[n++] = eight_first ? w4 : w8;
+  } else {
+    c[n++] = pk_config{1, cols, 0, 4, 1, 1, 1};
+  }
+  for (int i = 0; i < n && i < cap; ++i) out[i] = c[i];
+  return n;
+}
+
+bool row_config_listed(bool softmax, int rows, int cols, const pk_config &want) {
+  pk_config c[2];
+  const int n = row_configs(softmax, rows, cols, c, 2);
+  for (int i = 0; i < n; ++i)
+    if (std::memcmp(&c[i], &want, sizeof want) == 0) return true;
+  return false;
+}
+
+// Launch the kernel a listed config names (vec: the operands are 16-byte
+// aligned; a vector config needs that).
+template <bool RESID>
+int rmsnorm_run(const RowArgs &a, const pk_config &c, hipStream_t st) {
+  if (c.vector_width == 1) {
+    rmsnorm_generic_kernel<RESID><<<a.rows, kBlock, 0, st>>>(a);
+    return PK_OK;
+  }
+  const unsigned rows = (unsigned)a.rows;
+  if (c.block_m == 4) {
+    const dim3 grid(rows / 4 + (rows % 4 != 0));
+    switch (c.unroll) {
+      case 1: rmsnorm_vec_kernel<1, 1, RESID><<<grid, kBlock, 0, st>>>(a); return PK_OK;
+      case 2: rmsnorm_vec_kernel<1, 2, RESID><<<grid, kBlock, 0, st>>>(a); return PK_OK;
+      case 4: rmsnorm_vec_kernel<1, 4, RESID><<<grid, kBlock, 0, st>>>(a); return PK_OK;
+      case 8: rmsnorm_vec_kernel<1, 8, RESID><<<grid, kBlock, 0, st>>>(a); return PK_OK;
+    }
+  } else if (c.num_warps == 4) {
+    switch (c.unroll) {
+      case 4: rmsnorm_vec_kernel<4, 4, RESID><<<rows, 256, 0, st>>>(a); return PK_OK;
+      case 8: rmsnorm_vec_kernel<4, 8, RESID><<<rows, 256, 0, st>>>(a); return PK_OK;
+    }
+  } else if (c.num_warps == 8) {
+    switch (c.unroll) {
+      case 2: rmsnorm_vec_kernel<8, 2, RESID><<<rows, 512, 0, st>>>(a); return PK_OK;
+      case 4: rmsnorm_vec_kernel<8, 4, RESID><<<rows, 512, 0, st>>>(a); return PK_OK;
+    }
+  }
+  set_error("rmsnorm: config {%d, %d, %d, %d, %d, %d, %d} has no kernel", c.block_m, c.block_n, c.block_k,
+            c.num_warps, c.vector_width, c.unroll, c.shared_memory_stages);
+  return PK_ERR_UNSUPPORTED;
+}
+
 template <int MODE>
-int softmax_dispatch(const void *in, const uint16_t *mask, uint16_t *y, int rows, int cols,
+int softmax_run(const RowArgs &a, const pk_config &c, hipStream_t st) {
+  if (c.vector_width == 1) {
+    softmax_generic_kernel<MODE><<<a.rows, kBlock, 0, st>>>(a);
+    return PK_OK;
+  }
+  const unsigned rows = (unsigned)a.rows;
+  if (c.block_m == 4) {
+    const dim3 grid(rows / 4 + (rows % 4 != 0));
+    switch (c.unroll) {
+      case 1: softmax_vec_kernel<1, 1, MODE><<<grid, kBlock, 0, st>>>(a); return PK_OK;
+      case 2: softmax_vec_kernel<1, 2, MODE><<<grid, kBlock, 0, st>>>(a); return PK_OK;
+      case 4: softmax_vec_kernel<1, 4, MODE><<<grid, kBlock, 0, st>>>(a); return PK_OK;
+    }
+  } else if (c.num_warps == 4) {
+    switch (c.unroll) {
+      case 2: softmax_vec_kernel<4, 2, MODE><<<rows, 256, 0, st>>>(a); return PK_OK;
+      case 4: softmax_vec_kernel<4, 4, MODE><<<rows, 256, 0, st>>>(a); return PK_OK;
+      case 8: softmax_vec_kernel<4, 8, MODE><<<rows, 256, 0, st>>>(a); return PK_OK;
+    }
+  } else if (c.num_warps == 8) {
+    switch (c.unroll) {
+      case 1: softmax_vec_kernel<8, 1, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
+      case 2: softmax_vec_kernel<8, 2, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
+      case 4: softmax_vec_kernel<8, 4, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
+    }
+  }
+  set_error("softmax: config {%d, %d, %d, %d, %d, %d, %d} has no kernel", c.block_m, c.block_n, c.block_k,
+            c.num_warps, c.vector_width, c.unroll, c.shared_memory_stages);
+  return PK_ERR_UNSUPPORTED;
+}
+
+// cfg null: the built-in choice (the first candidate, or the generic kernel
+// when the operands are not 16-byte aligned); otherwise a listed config, which
+// must be the generic one when they are not.
+template <bool RESID>
+int rmsnorm_dispatch(const uint16_t *x, const uint16_t *r, const uint16_t *w, uint16_t *y, int rows, int cols,
+                     float eps, const pk_config *cfg, hipStream_t st, const char *name) {
+  PK_CHECK_ARG(x && y && (!RESID || r), "%s: null tensor pointer", name);
+  PK_CHECK_ARG(rows >= 0 && cols > 0, "%s: invalid shape rows=%d cols=%d", name, rows, cols);
+  PK_CHECK_ARG(!cfg || row_config_listed(false, std::max(rows, 1), cols, *cfg),
+               "%s: config {%d, %d, %d, %d, %d, %d, %d} is not a row config for cols=%d", name,
+               cfg ? cfg->block_m : 0, cfg ? cfg->block_n : 0, cfg ? cfg->block_k : 0, cfg ? cfg->num_warps : 0,
+               cfg ? cfg->vector_width : 0, cfg ? cfg->unroll : 0, cfg ? cfg->shared_memory_stages : 0, cols);
+  const bool aligned = aligned16(x) && aligned16(y) && (!RESID || aligned16(r)) && (!w || aligned16(w));
+  if (cfg && cfg->vector_width == 8 && !aligned) {
+    set_error("%s: the vector config needs 16-byte aligned x, r, gamma and out", name);
+    return PK_ERR_UNSUPPORTED;
+  }
+  if (rows == 0) return PK_OK;
+  const RowArgs a{x, RESID ? r : nullptr, w, y, rows, cols, 1.0f / (float)cols, eps};
+  pk_config c;
+  if (cfg) {
+    c = *cfg;
+  } else {
+    row_configs(false, rows, cols, &c, 1);
+    if (!aligned) c = pk_config{1, cols, 0, 4, 1, 1, 1};
+  }
+  int rc = rmsnorm_run<RESID>(a, c, st);
+  if (rc) return rc;
+  PK_LAUNCH_CHECK(name);
+  return PK_OK;
+}
+
+template <int MODE>
+int softmax_dispatch(const void *in, const uint16_t *mask, uint16_t *y, int rows, int cols, const pk_config *cfg,
                      hipStream_t st, const char *name) {
   PK_CHECK_ARG(in && y && (MODE == 0 || mask), "%s: null tensor pointer", name);
   PK_CHECK_ARG(rows >= 0 && cols > 0, "%s: invalid shape rows=%d cols=%d", name, rows, cols);
+  PK_CHECK_ARG(!cfg || row_config_listed(true, std::max(rows, 1), cols, *cfg),
+               "%s: config {%d, %d, %d, %d, %d, %d, %d} is not a row config for cols=%d", name,
+               cfg ? cfg->block_m : 0, cfg ? cfg->block_n : 0, cfg ? cfg->block_k : 0, cfg ? cfg->num_warps : 0,
+               cfg ? cfg->vector_width : 0, cfg ? cfg->unroll : 0, cfg ? cfg->shared_memory_stages : 0, cols);
+  const bool aligned = aligned16(in) && aligned16(y) && (MODE == 0 || aligned16(mask));
+  if (cfg && cfg->vector_width == 8 && !aligned) {
+    set_error("%s: the vector config needs 16-byte aligned input, mask and out", name);
+    return PK_ERR_UNSUPPORTED;
+  }
   if (rows == 0) return PK_OK;
   const RowArgs a{in, MODE == 0 ? nullptr : mask, nullptr, y, rows, cols, 0.f, 0.f};
-  const bool vec = (cols % 8 == 0) && aligned16(in) && aligned16(y) && (MODE == 0 || aligned16(mask));
-  const int nvec = cols / 8;
-  if (vec && nvec <= 64 * 4) {
-    const dim3 grid(rows / 4 + (rows % 4 != 0));
-#define PK_SM_W(VPT) softmax_vec_kernel<1, VPT, MODE><<<grid, kBlock, 0, st>>>(a)
-    if (nvec <= 64) PK_SM_W(1);
-    else if (nvec <= 128) PK_SM_W(2);
-    else PK_SM_W(4);
-#undef PK_SM_W
-  } else if (vec && nvec <= 256 * 8) {
-    const dim3 grid(rows);
-#define PK_SM_B(VPT) softmax_vec_kernel<4, VPT, MODE><<<grid, kBlock, 0, st>>>(a)
-    if (nvec <= 256 * 2) PK_SM_B(2);
-    else if (nvec <= 256 * 4) PK_SM_B(4);
-    else PK_SM_B(8);
-#undef PK_SM_B
+  pk_config c;
+  if (cfg) {
+    c = *cfg;
   } else {
-    softmax_generic_kernel<MODE><<<rows, kBlock, 0, st>>>(a);
+    row_configs(true, rows, cols, &c, 1);
+    if (!aligned) c = pk_config{1, cols, 0, 4, 1, 1, 1};
   }
+  int rc = softmax_run<MODE>(a, c, st);
+  if (rc) return rc;
   PK_LAUNCH_CHECK(name);
   return PK_OK;
 }
@@ -224,7 +341,7 @@ int grid_for(int64_t work, int per_thread = 1) {
 // exported to other translation units (mlp block)
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, int rows, int cols,
                    float eps, hipStream_t st) {
-  return rmsnorm_dispatch<false>(x, nullptr, w, y, rows, cols, eps, st, "rmsnorm");
+  return rmsnorm_dispatch<false>(x, nullptr, w, y, rows, cols, eps, nullptr, st, "rmsnorm");
 }
 
 int gelu_launch(const uint16_t *in, uint16_t *out, int64_t n, hipStream_t st) {
@@ -238,37 +355,11 @@ int gelu_launch(const uint16_t *in, uint16_t *out, int64_t n, hipStream_t st) {
   return PK_OK;
 }
 
-// The kernels the row-wise dispatchers above run for 16-byte aligned
-// operands, as configs: block_m = rows per workgroup (4: one wave per row;
-// 1: four waves per row), block_n = cols, num_warps = 4, vector_width = bf16
-// per load (8, or 1 for the generic kernel), unroll = 16-byte vectors per
-// lane, one pass over a register-resident row (block_k 0, stages 1).
-bool rmsnorm_config(int rows, int cols, pk_config *out) {
-  if (rows <= 0 || cols <= 0) return false;
-  const int nvec = cols / 8;
-  if (cols % 8 == 0 && nvec <= 64 * 8) {
-    const int vpt = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : 8;
-    *out = pk_config{4, cols, 0, kBlock / 64, 8, vpt, 1};
-  } else if (cols % 8 == 0 && nvec <= 256 * 8) {
-    *out = pk_config{1, cols, 0, kBlock / 64, 8, nvec <= 256 * 4 ? 4 : 8, 1};
-  } else {
-    *out = pk_config{1, cols, 0, kBlock / 64, 1, 1, 1};
-  }
-  return true;
-}
-
-bool softmax_config(int rows, int cols, pk_config *out) {
-  if (rows <= 0 || cols <= 0) return false;
-  const int nvec = cols / 8;
-  if (cols % 8 == 0 && nvec <= 64 * 4) {
-    *out = pk_config{4, cols, 0, kBlock / 64, 8, nvec <= 64 ? 1 : nvec <= 128 ? 2 : 4, 1};
-  } else if (cols % 8 == 0 && nvec <= 256 * 8) {
-    *out = pk_config{1, cols, 0, kBlock / 64, 8, nvec <= 256 * 2 ? 2 : nvec <= 256 * 4 ? 4 : 8, 1};
-  } else {
-    *out = pk_config{1, cols, 0, kBlock / 64, 1, 1, 1};
-  }
-  return true;
-}
+// The built-in choice for 16-byte aligned operands (the first candidate).
+bool rmsnorm_config(int rows, int cols, pk_config *out) { return row_configs(false, rows, cols, out, 1) > 0; }
+bool softmax_config(int rows, int cols, pk_config *out) { return row_configs(true, rows, cols, out, 1) > 0; }
+int rmsnorm_configs(int rows, int cols, pk_config *out, int cap) { return row_configs(false, rows, cols, out, cap); }
+int softmax_configs(int rows, int cols, pk_config *out, int cap) { return row_configs(true, rows, cols, out, cap); }
 
 }  // namespace pk
 
@@ -278,25 +369,37 @@ extern "C" {
 
 int launch_rmsnorm(const uint16_t *input, const uint16_t *weight, uint16_t *output, int rows,
                    int cols, float eps, void *stream) {
-  return rmsnorm_dispatch<false>(input, nullptr, weight, output, rows, cols, eps,
+  return rmsnorm_dispatch<false>(input, nullptr, weight, output, rows, cols, eps, nullptr,
                                  (hipStream_t)stream, "launch_rmsnorm");
 }
 
 int launch_fused_residual_rmsnorm(const uint16_t *x, const uint16_t *r, const uint16_t *gamma,
                                   uint16_t *out, int rows, int cols, float eps, void *stream) {
-  return rmsnorm_dispatch<true>(x, r, gamma, out, rows, cols, eps, (hipStream_t)stream,
+  return rmsnorm_dispatch<true>(x, r, gamma, out, rows, cols, eps, nullptr, (hipStream_t)stream,
                                 "launch_fused_residual_rmsnorm");
 }
 
+int pk_fused_residual_rmsnorm_config(const uint16_t *x, const uint16_t *r, const uint16_t *gamma, uint16_t *out,
+                                     int rows, int cols, float eps, const pk_config *cfg, void *stream) {
+  return rmsnorm_dispatch<true>(x, r, gamma, out, rows, cols, eps, cfg, (hipStream_t)stream,
+                                "pk_fused_residual_rmsnorm_config");
+}
+
 int launch_softmax(const uint16_t *input, uint16_t *output, int rows, int cols, void *stream) {
-  return softmax_dispatch<0>(input, nullptr, output, rows, cols, (hipStream_t)stream,
+  return softmax_dispatch<0>(input, nullptr, output, rows, cols, nullptr, (hipStream_t)stream,
                              "launch_softmax");
 }
 
 int launch_fused_softmax_mask(const float *logits, const uint16_t *mask, uint16_t *out, int rows,
                               int cols, void *stream) {
-  return softmax_dispatch<1>(logits, mask, out, rows, cols, (hipStream_t)stream,
+  return softmax_dispatch<1>(logits, mask, out, rows, cols, nullptr, (hipStream_t)stream,
                              "launch_fused_softmax_mask");
+}
+
+int pk_fused_softmax_mask_config(const float *logits, const uint16_t *mask, uint16_t *out, int rows, int cols,
+                                 const pk_config *cfg, void *stream) {
+  return softmax_dispatch<1>(logits, mask, out, rows, cols, cfg, (hipStream_t)stream,
+                             "pk_fused_softmax_mask_config");
 }
 
 int launch_gelu(const uint16_t *input, uint16_t *output, int n, void *stream) {

@@ -4,10 +4,10 @@
 // objects the emitter instantiates at a tuned configuration
 // (csrc/runtime/codegen.cpp).  Both compile this one source.
 //
-// One row per wave (short rows) or per 256-thread block (long rows), the row
-// held in registers so every input byte is read from HBM exactly once; 16-byte
-// vector loads/stores; wave64 shuffle reductions, then one LDS exchange across
-// the block's 4 waves.
+// One row per wave (short rows) or per block of NW = 4 or 8 waves (long rows),
+// the row held in registers so every input byte is read from HBM exactly once;
+// 16-byte vector loads/stores; wave64 shuffle reductions, then one LDS exchange
+// across the block's waves.
 #pragma once
 
 #include "pk_common.hpp"
@@ -83,8 +83,9 @@ __device__ __forceinline__ float group_max(float v, float *red) {
 
 // ---------------------------------------------------------------------------
 // RMSNorm / residual + RMSNorm (vector path: cols % 8 == 0, 16-byte aligned).
-// NW waves cooperate on one row (NW == 1: each wave owns a row, 4 rows per
-// block).  Each lane keeps VPT 8-element vectors of the row in registers.
+// NW waves cooperate on one row in a block of NW * 64 threads (NW == 1: each
+// wave owns a row, 4 rows per 256-thread block).  Each lane keeps VPT
+// 8-element vectors of the row in registers.
 // Arithmetic per kernels/cpu/cpu_reference.cpp:16-44: ss = sum x^2 (fp32),
 // rms = sqrt(ss * (1/cols) + eps), y = bf16((x / rms) [* w]).  With a residual
 // the normalised value is s = bf16(x + r) (tests/golden/golden.py:108-112).

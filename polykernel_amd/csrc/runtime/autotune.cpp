@@ -317,8 +317,8 @@ bool PrepareResidualRmsnorm(const Shape &s, const AutotuneOptions &o, DeviceAren
   w.out_elems = n;
   w.compare_n = (long long)n;
   w.golden = [=](hipStream_t st) { return pk_naive_rmsnorm(X[0], R[0], G[0], want, rows, cols, 1e-6f, st); };
-  w.run = [=](const pk_config *, int c, hipStream_t st) {
-    return launch_fused_residual_rmsnorm(X[c], R[c], G[c], w.out[c], rows, cols, 1e-6f, st);
+  w.run = [=](const pk_config *cfg, int c, hipStream_t st) {
+    return pk_fused_residual_rmsnorm_config(X[c], R[c], G[c], w.out[c], rows, cols, 1e-6f, cfg, st);
   };
   return true;
 }
@@ -347,8 +347,8 @@ bool PrepareSoftmaxMask(const Shape &s, const AutotuneOptions &o, DeviceArena &a
   w.out_elems = n;
   w.compare_n = (long long)n;
   w.golden = [=](hipStream_t st) { return pk_naive_softmax_mask(L[0], Mk[0], want, rows, cols, st); };
-  w.run = [=](const pk_config *, int c, hipStream_t st) {
-    return launch_fused_softmax_mask(L[c], Mk[c], w.out[c], rows, cols, st);
+  w.run = [=](const pk_config *cfg, int c, hipStream_t st) {
+    return pk_fused_softmax_mask_config(L[c], Mk[c], w.out[c], rows, cols, cfg, st);
   };
   return true;
 }

@@ -32,9 +32,10 @@
 //   and workspace decisions and launches the object's entry points.
 //   fused_residual_rmsnorm, fused_softmax_mask (rowwise_kernels.hpp):
 //     pk_row(pk_row_args)          the config's row kernel: vector_width 8 -- one wave per row
-//                                  (block_m 4, grid ceil(rows/4)) or four (block_m 1, grid rows)
+//                                  (block_m 4, grid ceil(rows/4), 256 threads) or num_warps waves
+//                                  per row (block_m 1, grid rows, 64 * num_warps threads, 4 or 8)
 //                                  with `unroll` 16-byte vectors per lane; vector_width 1 -- the
-//                                  generic kernel (grid rows); 256 threads
+//                                  generic kernel (grid rows, 256 threads)
 //     pk_row_any(pk_row_args)      the generic kernel, for operands the vector kernel cannot take
 //   fused_rmsnorm_matmul (gemm_kernels.hpp, rowwise_kernels.hpp):
 //     pk_panel(pk_panel_args)      block_k = K: the whole-K panel kernel (256 threads); num_warps 2:
@@ -107,22 +108,33 @@ bool GemmInstance(const Config &c, int epi, std::string &body, int &threads) {
 // four) with VPT = unroll vectors per lane; vector_width 1 -- the generic
 // kernel.  `kind` is the third template argument: RMSNorm's residual flag
 // ("true" / "false") or softmax's mode ("1": masked).
-bool RowInstance(const Config &c, bool softmax, const std::string &kind, std::string &body, std::string &any) {
+// The row kernel a config names: waves per row = 1 (block_m 4: 4 rows per
+// 256-thread block) or num_warps (block_m 1: a row per num_warps * 64 threads,
+// 4 or 8), unroll 16-byte vectors per lane; `threads` = the pk_row block size.
+bool RowInstance(const Config &c, bool softmax, const std::string &kind, std::string &body, std::string &any,
+                 int &threads) {
   const std::string ns = softmax ? "pk::row::softmax_" : "pk::row::rmsnorm_";
   any = ns + "generic_body<" + kind + ">";
-  if (c.num_warps != 4 || c.block_k != 0) return false;
+  threads = 256;
+  if (c.block_k != 0) return false;
   if (c.vector_width == 1) {
     body = any;
+    return c.num_warps == 4;
+  }
+  if (c.vector_width != 8 || c.unroll < 1 || c.unroll > 8) return false;
+  if (c.block_m == 4 && c.num_warps == 4) {
+    body = ns + "vec_body<1, " + std::to_string(c.unroll) + ", " + kind + ">";
     return true;
   }
-  if (c.vector_width != 8 || (c.block_m != 4 && c.block_m != 1) || c.unroll < 1 || c.unroll > 8) return false;
-  body = ns + "vec_body<" + std::to_string(c.block_m == 4 ? 1 : 4) + ", " + std::to_string(c.unroll) + ", " + kind +
-         ">";
+  if (c.block_m != 1 || (c.num_warps != 4 && c.num_warps != 8)) return false;
+  threads = 64 * c.num_warps;
+  body = ns + "vec_body<" + std::to_string(c.num_warps) + ", " + std::to_string(c.unroll) + ", " + kind + ">";
   return true;
 }
 
-std::string RowEntryPoints(const std::string &body, const std::string &any) {
-  return "extern \"C\" __global__ __launch_bounds__(256) void pk_row(pk_row_args a) {\n  " + body +
+std::string RowEntryPoints(const std::string &body, const std::string &any, int threads) {
+  return "extern \"C\" __global__ __launch_bounds__(" + std::to_string(threads) +
+         ") void pk_row(pk_row_args a) {\n  " + body +
          "(a);\n}\n\nextern \"C\" __global__ __launch_bounds__(256) void pk_row_any(pk_row_args a) {\n  " + any +
          "(a);\n}\n";
 }
@@ -192,11 +204,12 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
                            "\n// config: " + autotune::ToString(c) + "\n";
   if (rms || smx) {
     std::string body, any;
-    if (!RowInstance(c, smx, smx ? "1" : "true", body, any)) {
+    int threads = 0;
+    if (!RowInstance(c, smx, smx ? "1" : "true", body, any, threads)) {
       error = "config {" + autotune::ToString(c) + "} has no row kernel template";
       return false;
     }
-    source = head + "#include \"rowwise_kernels.hpp\"\n\n" + RowEntryPoints(body, any);
+    source = head + "#include \"rowwise_kernels.hpp\"\n\n" + RowEntryPoints(body, any, threads);
     return true;
   }
   if (panel) {
@@ -216,17 +229,17 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
     // config into workspace, then the config's GEMM
     pk_config rc{};
     std::string rbody, rany, gbody;
-    int threads = 0;
+    int threads = 0, rthreads = 0;
     if (pk_op_default_config("fused_residual_rmsnorm", e.shape.m, e.shape.k, 0, &rc) != PK_OK ||
         !RowInstance(Config{rc.block_m, rc.block_n, rc.block_k, rc.num_warps, rc.vector_width, rc.unroll,
                             rc.shared_memory_stages},
-                     false, "false", rbody, rany) ||
+                     false, "false", rbody, rany, rthreads) ||
         !GemmInstance(c, 0, gbody, threads)) {
       error = "config {" + autotune::ToString(c) + "} has no RMSNorm -> GEMM kernel template";
       return false;
     }
     source = head + "#include \"gemm_kernels.hpp\"\n#include \"rowwise_kernels.hpp\"\n\n" +
-             RowEntryPoints(rbody, rany) + "\nextern \"C\" __global__ __launch_bounds__(" + std::to_string(threads) +
+             RowEntryPoints(rbody, rany, rthreads) + "\nextern \"C\" __global__ __launch_bounds__(" + std::to_string(threads) +
              (c.block_k == 32 ? ", 1" : "") + ") void pk_gemm(pk_gemm_args g) {\n  " + gbody + "(g);\n}\n";
     return true;
   }

@@ -278,12 +278,15 @@ std::optional<CachedBinary> BinaryOf(const ModuleTable &table, const CacheEntry 
 // Launch a row object (pk_row, pk_row_any) on a [rows, cols] argument block
 // as rowwise.hip's dispatchers launch the linked kernels: the config's
 // vector kernel when it is one (vector_width 8) and the operands are 16-byte
-// aligned with cols % 8 == 0, else the generic kernel, one block per row.
+// aligned with cols % 8 == 0 -- 4 rows per 256-thread block (block_m 4) or a
+// row per block of num_warps waves -- else the generic kernel, a row per
+// 256-thread block.
 bool RowLaunch(ModuleTable::Loaded *mod, const Config &c, pk_row_args a, void *stream, std::string &error) {
   const bool vec = c.vector_width == 8 && a.cols % 8 == 0 && Aligned16(a.in) && Aligned16(a.out) &&
                    (!a.aux || Aligned16(a.aux)) && (!a.gamma || Aligned16(a.gamma));
   const unsigned grid = vec && c.block_m == 4 ? (unsigned)(a.rows / 4 + (a.rows % 4 != 0)) : (unsigned)a.rows;
-  return ModuleLaunch(mod->fns[vec ? 0 : 1], grid, 1, 256, stream, a, vec ? "pk_row" : "pk_row_any", error);
+  const unsigned threads = vec && c.block_m == 1 ? 64u * (unsigned)c.num_warps : 256u;
+  return ModuleLaunch(mod->fns[vec ? 0 : 1], grid, 1, threads, stream, a, vec ? "pk_row" : "pk_row_any", error);
 }
 
 // Row-op code objects: residual + RMSNorm and masked softmax.
@@ -464,13 +467,21 @@ void RegisterBuiltinLaunchers(Runtime &rt) {
   rt.RegisterLauncher("fused_residual_rmsnorm", [](const CacheEntry &e, void *io, std::string &error) {
     ResidualRmsnormIO *p = Cast<ResidualRmsnormIO>(io, error);
     if (!p || !CheckEntry(e, p->rows, p->cols, 0, error)) return false;
-    return Launched(
-        launch_fused_residual_rmsnorm(p->x, p->r, p->gamma, p->out, p->rows, p->cols, p->eps, p->stream), e, error);
+    // the entry's config; operands that are not 16-byte aligned take the generic kernel
+    const pk_config cfg = ToPk(e.best);
+    const bool aligned = Aligned16(p->x) && Aligned16(p->r) && Aligned16(p->out) && (!p->gamma || Aligned16(p->gamma));
+    return Launched(pk_fused_residual_rmsnorm_config(p->x, p->r, p->gamma, p->out, p->rows, p->cols, p->eps,
+                                                     aligned ? &cfg : nullptr, p->stream),
+                    e, error);
   });
   rt.RegisterLauncher("fused_softmax_mask", [](const CacheEntry &e, void *io, std::string &error) {
     SoftmaxMaskIO *p = Cast<SoftmaxMaskIO>(io, error);
     if (!p || !CheckEntry(e, p->rows, p->cols, 0, error)) return false;
-    return Launched(launch_fused_softmax_mask(p->logits, p->mask, p->out, p->rows, p->cols, p->stream), e, error);
+    const pk_config cfg = ToPk(e.best);
+    const bool aligned = Aligned16(p->logits) && Aligned16(p->mask) && Aligned16(p->out);
+    return Launched(pk_fused_softmax_mask_config(p->logits, p->mask, p->out, p->rows, p->cols,
+                                                 aligned ? &cfg : nullptr, p->stream),
+                    e, error);
   });
   rt.RegisterLauncher("fused_kv_append_attention", [](const CacheEntry &e, void *io, std::string &error) {
     KvAppendAttentionIO *p = Cast<KvAppendAttentionIO>(io, error);

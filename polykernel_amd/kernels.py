@@ -52,16 +52,23 @@ def rmsnorm(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float =
 
 
 def fused_residual_rmsnorm(x: torch.Tensor, residual: torch.Tensor,
-                           weight: Optional[torch.Tensor] = None, eps: float = 1e-5) -> torch.Tensor:
-    """golden.fused_residual_rmsnorm (golden.py:108-112)."""
+                           weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
+                           config: Optional[dict] = None) -> torch.Tensor:
+    """golden.fused_residual_rmsnorm (golden.py:108-112); `config` picks one of
+    pk_op_configs("fused_residual_rmsnorm", rows, cols, 0) (tuning/test hook
+    pk_fused_residual_rmsnorm_config)."""
     if x.shape != residual.shape:
         raise ValueError("x and residual must have the same shape")
     cols = x.shape[-1]
     rows = x.numel() // cols
     out = torch.empty_like(x)
-    check(_lib.load().launch_fused_residual_rmsnorm(
-        _dev(x, bf16, "x"), _dev(residual, bf16, "residual"), _opt(weight, bf16, "weight"),
-        _dev(out, bf16, "out"), rows, cols, eps, _stream()), "launch_fused_residual_rmsnorm")
+    args = (_dev(x, bf16, "x"), _dev(residual, bf16, "residual"), _opt(weight, bf16, "weight"),
+            _dev(out, bf16, "out"), rows, cols, eps)
+    if config is None:
+        check(_lib.load().launch_fused_residual_rmsnorm(*args, _stream()), "launch_fused_residual_rmsnorm")
+    else:
+        check(_lib.load().pk_fused_residual_rmsnorm_config(*args, _lib.Config(**config), _stream()),
+              "pk_fused_residual_rmsnorm_config")
     return out
 
 
@@ -82,15 +89,21 @@ def softmax(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def fused_softmax_mask(logits: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-    """golden.fused_softmax_mask (golden.py:115-117) on fp32 logits + bf16 additive mask."""
+def fused_softmax_mask(logits: torch.Tensor, mask: torch.Tensor, config: Optional[dict] = None) -> torch.Tensor:
+    """golden.fused_softmax_mask (golden.py:115-117) on fp32 logits + bf16 additive mask;
+    `config` picks one of pk_op_configs("fused_softmax_mask", rows, cols, 0)
+    (tuning/test hook pk_fused_softmax_mask_config)."""
     if logits.shape != mask.shape:
         raise ValueError("logits and mask must have the same shape")
     cols = logits.shape[-1]
     out = torch.empty(logits.shape, dtype=bf16, device=logits.device)
-    check(_lib.load().launch_fused_softmax_mask(
-        _dev(logits, torch.float32, "logits"), _dev(mask, bf16, "mask"), _dev(out, bf16, "out"),
-        logits.numel() // cols, cols, _stream()), "launch_fused_softmax_mask")
+    args = (_dev(logits, torch.float32, "logits"), _dev(mask, bf16, "mask"), _dev(out, bf16, "out"),
+            logits.numel() // cols, cols)
+    if config is None:
+        check(_lib.load().launch_fused_softmax_mask(*args, _stream()), "launch_fused_softmax_mask")
+    else:
+        check(_lib.load().pk_fused_softmax_mask_config(*args, _lib.Config(**config), _stream()),
+              "pk_fused_softmax_mask_config")
     return out
 
 

@@ -84,15 +84,28 @@ def test_emit_source_row_templates():
     as the second entry point for unaligned operands."""
     for op, body, any_ in (("fused_residual_rmsnorm", "rmsnorm_vec_body", "rmsnorm_generic_body<true>"),
                            ("fused_softmax_mask", "softmax_vec_body", "softmax_generic_body<1>")):
-        kind = "true" if op == "fused_residual_rmsnorm" else "1"
-        widths = {512: f"{body}<1, 1, {kind}>", 1024: f"{body}<1, 2, {kind}>", 8192: f"{body}<4, 4, {kind}>",
-                  16384: f"{body}<4, 8, {kind}>", 999: any_}
-        widths[4096] = f"{body}<1, 8, {kind}>" if op == "fused_residual_rmsnorm" else f"{body}<4, 2, {kind}>"
-        for cols, inst in widths.items():
+        rms = op == "fused_residual_rmsnorm"
+        kind = "true" if rms else "1"
+        # built-in choices: one wave per row for short rows, then a row per
+        # workgroup of 4 or 8 waves (8 for softmax, and for RMSNorm above 1024 vectors)
+        widths = {512: (1, 1), 1024: (1, 2), 4096: (1, 8) if rms else (8, 1), 8192: (4, 4) if rms else (8, 2),
+                  16384: (8, 4)}
+        for cols, (nw, vpt) in widths.items():
             src = rt.emit_source(row_entry(op, 64, cols))
-            assert f"void pk_row(pk_row_args a) {{\n  pk::row::{inst}(a);" in src, (op, cols, src)
+            threads = 256 if nw <= 4 else 64 * nw
+            assert (f"__launch_bounds__({threads}) void pk_row(pk_row_args a) {{\n  "
+                    f"pk::row::{body}<{nw}, {vpt}, {kind}>(a);") in src, (op, cols, src)
             assert f"void pk_row_any(pk_row_args a) {{\n  pk::row::{any_}(a);" in src, (op, cols)
             assert '#include "rowwise_kernels.hpp"' in src
+        src = rt.emit_source(row_entry(op, 64, 999))
+        assert f"void pk_row(pk_row_args a) {{\n  pk::row::{any_}(a);" in src
+        # every candidate of a long row (4 and 8 waves) has a template
+        for cols in (4096, 8192, 16384):
+            e = row_entry(op, 64, cols)
+            for cfg in rt.candidates(op, 64, cols, 0):
+                e["best"] = cfg
+                assert f"vec_body<{cfg['num_warps'] if cfg['block_m'] == 1 else 1}, {cfg['unroll']}, {kind}>" in \
+                    rt.emit_source(e), (op, cols, cfg)
 
 
 def test_emit_source_rmsnorm_matmul_templates():

@@ -180,6 +180,60 @@ def test_softmax_mask(gpu, oracle, rows, cols):
     assert np.all(f32(got)[mask == 0xFF80] == 0.0)
 
 
+@pytest.mark.parametrize("rows,cols", [(37, 2048), (37, 4096), (37, 6000), (37, 8192), (21, 12000), (37, 16384)])
+def test_row_ops_every_config(gpu, oracle, rows, cols):
+    """Every candidate of residual + RMSNorm and masked softmax (one wave per
+    row, a workgroup of 4 or 8 waves per row; ragged rows and widths that
+    leave lanes idle) through pk_*_config against the oracle."""
+    from polykernel_amd import runtime as rt
+
+    x, r = synth.normal_bf16((rows, cols), 3), synth.normal_bf16((rows, cols), 4)
+    g = synth.normal_bf16((cols,), 5, 0.1, 1.0)
+    logits, mask = synth.normal_f32((rows, cols), 7, 2.0), synth.mask_bf16((rows, cols), 8, 0.1)
+    want_r = oracle.residual_rmsnorm(x, r, g, 1e-6)
+    want_s = oracle.softmax_mask(logits, mask)
+    for op in ("fused_residual_rmsnorm", "fused_softmax_mask"):
+        cands = rt.candidates(op, rows, cols, 0)
+        assert cands and cands[0] == rt.default_config(op, rows, cols, 0)
+        for cfg in cands:
+            _say(f"{op} {rows}x{cols} {cfg}")
+            if op == "fused_residual_rmsnorm":
+                got = from_dev(K().fused_residual_rmsnorm(to_dev(x), to_dev(r), to_dev(g), 1e-6, config=cfg))
+                rep = mt.assert_correct(got, want_r, what=op)
+                assert rep.bit_exact >= 0.99 and rep.max_ulp <= 1, (cfg, rep)
+            else:
+                got = from_dev(K().fused_softmax_mask(to_dev(logits), to_dev(mask), config=cfg))
+                rep = mt.assert_correct(got, want_s, what=op)
+                assert rep.bit_exact >= 0.98, (cfg, rep)
+                assert np.all(f32(got)[mask == 0xFF80] == 0.0)
+
+
+def test_row_config_refusals(gpu):
+    """A config outside the shape's list is an argument error; a vector config
+    with operands that are not 16-byte aligned is refused (the built-in choice
+    then takes the generic kernel)."""
+    import torch
+    from polykernel_amd import _lib
+    from polykernel_amd import runtime as rt
+
+    lib = _lib.load()
+    rows, cols = 8, 8192
+    xs = torch.zeros(rows * cols + 8, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(rows * cols + 8, dtype=torch.bfloat16, device="cuda")
+    ptr = xs.data_ptr()
+    wrong = _lib.Config(4, cols, 0, 4, 8, 1, 1)  # one wave per row cannot hold 1024 vectors
+    rc = lib.pk_fused_residual_rmsnorm_config(ptr, ptr, None, out.data_ptr(), rows, cols, 1e-6, wrong, None)
+    assert rc == _lib.PK_ERR_INVALID_ARG and "is not a row config" in _lib.last_error()
+    cfg = _lib.Config(**rt.default_config("fused_residual_rmsnorm", rows, cols, 0))
+    rc = lib.pk_fused_residual_rmsnorm_config(ptr + 2, ptr + 2, None, out.data_ptr() + 2, rows, cols, 1e-6, cfg, None)
+    assert rc == _lib.PK_ERR_UNSUPPORTED and "16-byte aligned" in _lib.last_error()
+    logits = torch.zeros(rows * cols + 4, dtype=torch.float32, device="cuda")
+    cfg = _lib.Config(**rt.default_config("fused_softmax_mask", rows, cols, 0))
+    rc = lib.pk_fused_softmax_mask_config(logits.data_ptr() + 4, ptr, out.data_ptr(), rows, cols, cfg, None)
+    assert rc == _lib.PK_ERR_UNSUPPORTED and "16-byte aligned" in _lib.last_error()
+    torch.cuda.synchronize()
+
+
 def test_kv_cache_update_bit_exact(gpu, oracle):
     cache, new = rng_bf16((1, 4, 100, 128), 9), rng_bf16((1, 4, 28, 128), 10)
     got = from_dev(K().kv_cache_update(to_dev(cache), to_dev(new)))

@@ -615,14 +615,16 @@ def test_conformance_code_objects_bit_identical(gpu):
 
 def _row_served_equals_linked(served, e, seed):
     """A residual + RMSNorm or masked-softmax call served from its code object
-    equals the linked launcher bit for bit: with 16-byte aligned operands (the
-    config's kernel; RMSNorm with and without gamma) and with every operand
-    one element past alignment (both paths take the generic kernel)."""
+    equals the linked kernel at the same config bit for bit: with 16-byte
+    aligned operands (pk_*_config at the entry's config; RMSNorm with and
+    without gamma) and with every operand one element past alignment (both
+    paths take the generic kernel)."""
     import torch
 
     lib = _lib.load()
     op, rows, cols = e["op"], e["shape"]["M"], e["shape"]["N"]
     n = rows * cols + 8
+    cfg = C.byref(_cfg(e["best"]))
     for off in (0, 1):
         outs = [torch.zeros(n, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
         if op == "fused_softmax_mask":
@@ -631,8 +633,12 @@ def _row_served_equals_linked(served, e, seed):
             io = rt.SoftmaxMaskIO(logits=_ptr(lg[off:]), mask=_ptr(mk[off:]), out=_ptr(outs[0][off:]), rows=rows,
                                   cols=cols, stream=_stream())
             served.run(op, rows, cols, 0, io)
-            _lib.check(lib.launch_fused_softmax_mask(_ptr(lg[off:]), _ptr(mk[off:]), _ptr(outs[1][off:]), rows, cols,
-                                                     _stream()), op)
+            if off == 0:
+                _lib.check(lib.pk_fused_softmax_mask_config(_ptr(lg), _ptr(mk), _ptr(outs[1]), rows, cols, cfg,
+                                                            _stream()), op)
+            else:
+                _lib.check(lib.launch_fused_softmax_mask(_ptr(lg[off:]), _ptr(mk[off:]), _ptr(outs[1][off:]), rows,
+                                                         cols, _stream()), op)
         else:
             x, r = to_dev(synth.normal_bf16((n,), seed)), to_dev(synth.normal_bf16((n,), seed + 1))
             for gamma in (to_dev(synth.normal_bf16((cols + 8,), seed + 2, 0.1, 1.0)), None):
@@ -640,8 +646,12 @@ def _row_served_equals_linked(served, e, seed):
                 io = rt.ResidualRmsnormIO(x=_ptr(x[off:]), r=_ptr(r[off:]), gamma=_ptr(g), out=_ptr(outs[0][off:]),
                                           rows=rows, cols=cols, eps=1e-6, stream=_stream())
                 served.run(op, rows, cols, 0, io)
-                _lib.check(lib.launch_fused_residual_rmsnorm(_ptr(x[off:]), _ptr(r[off:]), _ptr(g),
-                                                             _ptr(outs[1][off:]), rows, cols, 1e-6, _stream()), op)
+                if off == 0:
+                    _lib.check(lib.pk_fused_residual_rmsnorm_config(_ptr(x), _ptr(r), _ptr(g), _ptr(outs[1]), rows,
+                                                                    cols, 1e-6, cfg, _stream()), op)
+                else:
+                    _lib.check(lib.launch_fused_residual_rmsnorm(_ptr(x[off:]), _ptr(r[off:]), _ptr(g),
+                                                                 _ptr(outs[1][off:]), rows, cols, 1e-6, _stream()), op)
                 torch.cuda.synchronize()
                 assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (op, cols, off, gamma is None)
         torch.cuda.synchronize()
