@@ -697,6 +697,47 @@ def test_fused_kv_append_attention_flash_path(gpu, oracle, Sc, D):
     assert _att_bound_bad(oracle, got, want, q, kfull, vfull, True) == 0, rep
 
 
+@pytest.mark.parametrize("D", [128, 96, 512])
+def test_attention_known_answers(gpu, D):
+    """Closed forms on the device, no oracle: one key gives O = V bit for bit;
+    zero keys give uniform weights, so O is the mean of the visible V (exact
+    when the count is a power of two, within one bf16 ulp otherwise); causal
+    outputs do not move when future keys and values change.  D 128 takes the
+    flash kernel, 96 the generic one, 512 the wide one."""
+    from polykernel_amd.synth import f32_to_bf16
+
+    def run(q, k, v, causal):
+        return from_dev(K().attention_prefill(to_dev(q), to_dev(k), to_dev(v), None, causal))
+
+    q, k, v = rng_bf16((1, 4, 1, D), 80), rng_bf16((1, 4, 1, D), 81), rng_bf16((1, 4, 1, D), 82)
+    for causal in (False, True):
+        assert np.array_equal(run(q, k, v, causal), v), (D, causal)
+    # zero keys: non-causal over 64 keys (mean exact), causal over i + 1 keys
+    q = rng_bf16((1, 2, 16, D), 83)
+    k = np.zeros((1, 2, 64, D), np.uint16)
+    v = int_bf16((1, 2, 64, D), 84)
+    want = f32_to_bf16((f32(v).astype(np.float64).sum(axis=2, keepdims=True) / 64).astype(np.float32))
+    assert np.array_equal(run(q, k, v, False), np.broadcast_to(want, (1, 2, 16, D))), D
+    n = 40
+    q, k, v = rng_bf16((1, 2, n, D), 85), np.zeros((1, 2, n, D), np.uint16), int_bf16((1, 2, n, D), 86)
+    got = f32(run(q, k, v, True)).astype(np.float64)
+    csum = np.cumsum(f32(v).astype(np.float64), axis=2)
+    cnt = np.arange(1, n + 1, dtype=np.float64)[None, None, :, None]
+    mean = csum / cnt
+    ulp = np.maximum(np.abs(mean), 2.0**-126) * 2.0**-7
+    assert np.all(np.abs(got - mean) <= ulp), D
+    pow2 = np.array([(i + 1) & i == 0 for i in range(n)])
+    assert np.array_equal(got[:, :, pow2], f32(f32_to_bf16(mean[:, :, pow2].astype(np.float32)))), D
+    # future keys and values do not reach earlier queries
+    n, cut = 100, 60
+    q, k, v = rng_bf16((1, 2, n, D), 87), rng_bf16((1, 2, n, D), 88), rng_bf16((1, 2, n, D), 89)
+    k2, v2 = k.copy(), v.copy()
+    k2[:, :, cut:], v2[:, :, cut:] = rng_bf16((1, 2, n - cut, D), 90), rng_bf16((1, 2, n - cut, D), 91)
+    a, b = run(q, k, v, True), run(q, k2, v2, True)
+    assert np.array_equal(a[:, :, :cut], b[:, :, :cut]), D
+    assert not np.array_equal(a[:, :, cut:], b[:, :, cut:]), D
+
+
 def test_attention_leaky_mask_is_detected(gpu, oracle):
     q, k, v = rng_bf16((1, 2, 64, 64), 73), rng_bf16((1, 2, 64, 64), 74), rng_bf16((1, 2, 64, 64), 75)
     leak = from_dev(K().attention_prefill(to_dev(q), to_dev(k), to_dev(v), None, False))
