@@ -288,6 +288,17 @@ def test_gemm_integer_inputs_bit_exact(gpu, oracle, tile, M, N, Kd):
     assert np.array_equal(got, oracle.matmul(a, b))
 
 
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3])
+@pytest.mark.parametrize("M,N,Kd", [(1, 1, 1), (1, 8, 32), (3, 7, 5), (2, 264, 64), (257, 9, 96)])
+def test_gemm_tiny_shapes_bit_exact(gpu, oracle, tile, M, N, Kd):
+    """Degenerate but valid shapes (a single row, column or k, tiles mostly
+    outside the matrix) on every tile choice, integer inputs: bit-exact."""
+    _say(f"gemm tiny tile={tile} {M}x{N}x{Kd}")
+    a, b = int_bf16((M, Kd), 16), int_bf16((Kd, N), 17)
+    got = from_dev(K().gemm_ex(0, to_dev(a), to_dev(b), tile=tile))
+    assert np.array_equal(got, oracle.matmul(a, b)), (tile, M, N, Kd)
+
+
 def test_matmul_known_2x2(gpu):
     got = f32(from_dev(K().matmul(to_dev(bf([[1, 2], [3, 4]])), to_dev(bf([[5, 6], [7, 8]])))))
     assert np.array_equal(got, np.array([[19, 22], [43, 50]], np.float32))
@@ -736,6 +747,20 @@ def test_attention_known_answers(gpu, D):
     a, b = run(q, k, v, True), run(q, k2, v2, True)
     assert np.array_equal(a[:, :, :cut], b[:, :, :cut]), D
     assert not np.array_equal(a[:, :, cut:], b[:, :, cut:]), D
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("H,Skv,D", [(8, 777, 128), (8, 4096, 64), (4, 2000, 96), (2, 1500, 512)])
+def test_attention_single_query(gpu, oracle, H, Skv, D, causal):
+    """One query over a long key range (a decode step): the grid is one query
+    tile per head, so the key range is split over workgroups and merged."""
+    _say(f"attention single query H={H} Skv={Skv} D={D} causal={causal}")
+    q, k, v = rng_bf16((1, H, 1, D), 92), rng_bf16((1, H, Skv, D), 93), rng_bf16((1, H, Skv, D), 94)
+    got = from_dev(K().attention_prefill(to_dev(q), to_dev(k), to_dev(v), None, causal))
+    want = oracle.attention_prefill(q, k, v, None, causal)
+    rep = mt.report(got, want)
+    assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+    assert _att_bound_bad(oracle, got, want, q, k, v, causal) == 0, rep
 
 
 def test_attention_leaky_mask_is_detected(gpu, oracle):
