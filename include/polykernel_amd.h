@@ -224,10 +224,11 @@ PK_API int pk_gemm_ex(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C
  *     and of the V ring); other D: the generic kernel's one configuration.
  *   fused_residual_rmsnorm, fused_softmax_mask (shape rows, cols, 0):
  *     block_m = rows per workgroup (4: one wave per row; 1: one row per
- *     workgroup of num_warps = 4 or 8 waves), block_n = cols, unroll =
+ *     workgroup of num_warps = 4, 8 or 16 waves), block_n = cols, unroll =
  *     16-byte vectors per lane, vector_width 8 (1: the generic kernel for
- *     any cols), block_k 0, shared_memory_stages 1; long rows list the 4-
- *     and the 8-wave layout (pk_fused_*_config runs either).
+ *     any cols), block_k 0, shared_memory_stages 1; long rows list two
+ *     layouts (4 and 8 waves up to 16384 columns, 16 and 8 up to 65536;
+ *     pk_fused_*_config runs either).
  *   fused_rmsnorm_matmul: one fixed configuration per shape that describes
  *     the kernel the entry point runs (see pk_op_configs). */
 typedef struct pk_config {

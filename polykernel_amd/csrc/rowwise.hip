@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void softmax_generic_kernel(RowArgs a) {
 
 // ---- configurations ---------------------------------------------------------
 // A row config: block_m = rows per workgroup (4: one wave per row; 1: one
-// row per workgroup of num_warps waves, 4 or 8), block_n = cols, num_warps,
+// row per workgroup of num_warps waves, 4, 8 or 16), block_n = cols, num_warps,
 // vector_width = bf16 per load (8; 1 for the generic kernel, any cols and
 // alignment), unroll = 16-byte vectors per lane (the row stays in
 // registers), block_k 0 and stages 1.  Candidates, the built-in choice first:
@@ -68,9 +68,13 @@ __global__ __launch_bounds__(kBlock) void softmax_generic_kernel(RowArgs a) {
 //   (8 first for softmax and for RMSNorm rows above 1024 vectors -- measured
 //   on [16384, 8192]: masked softmax 168.9 -> 162.0 us, residual+RMSNorm equal;
 //   at 16384 columns 174.2 -> 171.8 and 136.5 -> 128.0 us);
+//   2049 to 8192 vectors (up to 65536 columns): 16 waves first, then 8 (the row
+//   still fits in registers: measured at 32768 columns residual+RMSNorm 478 ->
+//   136 us and masked softmax 621 -> 184 us against the generic kernel, at
+//   65536 columns 491 -> 176 and 622 -> 238 us, [rows, cols] of 2^27 elements);
 //   cols % 8 != 0 or longer rows: the generic kernel.
 int row_vpt(int nvec, int lanes) {
-  for (int v : {1, 2, 4, 8})
+  for (int v : {1, 2, 4, 8, 16})
     if (lanes * v >= nvec) return v;
   return 0;
 }
@@ -90,6 +94,11 @@ int row_configs(bool softmax, int rows, int cols, pk_config *out, int cap) {
     const bool eight_first = softmax || nvec > 1024;
     c[n++] = eight_first ? w8 : w4;
     c[n++] = eight_first ? w4 : w8;
+  } else if (cols % 8 == 0 && nvec <= 8192) {
+    // up to 65536 columns: 16 waves (a 1024-thread workgroup) with 4 or 8
+    // vectors per lane first, 8 waves with 8 or 16 second
+    c[n++] = pk_config{1, cols, 0, 16, 8, std::max(4, row_vpt(nvec, 1024)), 1};
+    c[n++] = pk_config{1, cols, 0, 8, 8, std::max(8, row_vpt(nvec, 512)), 1};
   } else {
     c[n++] = pk_config{1, cols, 0, 4, 1, 1, 1};
   }
@@ -131,6 +140,13 @@ int rmsnorm_run(const RowArgs &a, const pk_config &c, hipStream_t st) {
     switch (c.unroll) {
       case 2: rmsnorm_vec_kernel<8, 2, RESID><<<rows, 512, 0, st>>>(a); return PK_OK;
       case 4: rmsnorm_vec_kernel<8, 4, RESID><<<rows, 512, 0, st>>>(a); return PK_OK;
+      case 8: rmsnorm_vec_kernel<8, 8, RESID><<<rows, 512, 0, st>>>(a); return PK_OK;
+      case 16: rmsnorm_vec_kernel<8, 16, RESID><<<rows, 512, 0, st>>>(a); return PK_OK;
+    }
+  } else if (c.num_warps == 16) {
+    switch (c.unroll) {
+      case 4: rmsnorm_vec_kernel<16, 4, RESID><<<rows, 1024, 0, st>>>(a); return PK_OK;
+      case 8: rmsnorm_vec_kernel<16, 8, RESID><<<rows, 1024, 0, st>>>(a); return PK_OK;
     }
   }
   set_error("rmsnorm: config {%d, %d, %d, %d, %d, %d, %d} has no kernel", c.block_m, c.block_n, c.block_k,
@@ -163,6 +179,13 @@ int softmax_run(const RowArgs &a, const pk_config &c, hipStream_t st) {
       case 1: softmax_vec_kernel<8, 1, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
       case 2: softmax_vec_kernel<8, 2, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
       case 4: softmax_vec_kernel<8, 4, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
+      case 8: softmax_vec_kernel<8, 8, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
+      case 16: softmax_vec_kernel<8, 16, MODE><<<rows, 512, 0, st>>>(a); return PK_OK;
+    }
+  } else if (c.num_warps == 16) {
+    switch (c.unroll) {
+      case 4: softmax_vec_kernel<16, 4, MODE><<<rows, 1024, 0, st>>>(a); return PK_OK;
+      case 8: softmax_vec_kernel<16, 8, MODE><<<rows, 1024, 0, st>>>(a); return PK_OK;
     }
   }
   set_error("softmax: config {%d, %d, %d, %d, %d, %d, %d} has no kernel", c.block_m, c.block_n, c.block_k,

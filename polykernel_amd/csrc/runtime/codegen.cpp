@@ -33,7 +33,7 @@
 //   fused_residual_rmsnorm, fused_softmax_mask (rowwise_kernels.hpp):
 //     pk_row(pk_row_args)          the config's row kernel: vector_width 8 -- one wave per row
 //                                  (block_m 4, grid ceil(rows/4), 256 threads) or num_warps waves
-//                                  per row (block_m 1, grid rows, 64 * num_warps threads, 4 or 8)
+//                                  per row (block_m 1, grid rows, 64 * num_warps threads, 4/8/16)
 //                                  with `unroll` 16-byte vectors per lane; vector_width 1 -- the
 //                                  generic kernel (grid rows, 256 threads)
 //     pk_row_any(pk_row_args)      the generic kernel, for operands the vector kernel cannot take
@@ -110,7 +110,7 @@ bool GemmInstance(const Config &c, int epi, std::string &body, int &threads) {
 // ("true" / "false") or softmax's mode ("1": masked).
 // The row kernel a config names: waves per row = 1 (block_m 4: 4 rows per
 // 256-thread block) or num_warps (block_m 1: a row per num_warps * 64 threads,
-// 4 or 8), unroll 16-byte vectors per lane; `threads` = the pk_row block size.
+// 4, 8 or 16), unroll 16-byte vectors per lane; `threads` = the pk_row block size.
 bool RowInstance(const Config &c, bool softmax, const std::string &kind, std::string &body, std::string &any,
                  int &threads) {
   const std::string ns = softmax ? "pk::row::softmax_" : "pk::row::rmsnorm_";
@@ -121,12 +121,12 @@ bool RowInstance(const Config &c, bool softmax, const std::string &kind, std::st
     body = any;
     return c.num_warps == 4;
   }
-  if (c.vector_width != 8 || c.unroll < 1 || c.unroll > 8) return false;
+  if (c.vector_width != 8 || c.unroll < 1 || c.unroll > 16) return false;
   if (c.block_m == 4 && c.num_warps == 4) {
     body = ns + "vec_body<1, " + std::to_string(c.unroll) + ", " + kind + ">";
     return true;
   }
-  if (c.block_m != 1 || (c.num_warps != 4 && c.num_warps != 8)) return false;
+  if (c.block_m != 1 || (c.num_warps != 4 && c.num_warps != 8 && c.num_warps != 16) || c.unroll > 16) return false;
   threads = 64 * c.num_warps;
   body = ns + "vec_body<" + std::to_string(c.num_warps) + ", " + std::to_string(c.unroll) + ", " + kind + ">";
   return true;

@@ -89,7 +89,7 @@ def test_emit_source_row_templates():
         # built-in choices: one wave per row for short rows, then a row per
         # workgroup of 4 or 8 waves (8 for softmax, and for RMSNorm above 1024 vectors)
         widths = {512: (1, 1), 1024: (1, 2), 4096: (1, 8) if rms else (8, 1), 8192: (4, 4) if rms else (8, 2),
-                  16384: (8, 4)}
+                  16384: (8, 4), 32768: (16, 4), 65536: (16, 8)}
         for cols, (nw, vpt) in widths.items():
             src = rt.emit_source(row_entry(op, 64, cols))
             threads = 256 if nw <= 4 else 64 * nw
@@ -97,10 +97,11 @@ def test_emit_source_row_templates():
                     f"pk::row::{body}<{nw}, {vpt}, {kind}>(a);") in src, (op, cols, src)
             assert f"void pk_row_any(pk_row_args a) {{\n  pk::row::{any_}(a);" in src, (op, cols)
             assert '#include "rowwise_kernels.hpp"' in src
-        src = rt.emit_source(row_entry(op, 64, 999))
-        assert f"void pk_row(pk_row_args a) {{\n  pk::row::{any_}(a);" in src
-        # every candidate of a long row (4 and 8 waves) has a template
-        for cols in (4096, 8192, 16384):
+        for cols in (999, 70000):  # cols % 8 != 0, and rows longer than 65536 columns
+            src = rt.emit_source(row_entry(op, 64, cols))
+            assert f"void pk_row(pk_row_args a) {{\n  pk::row::{any_}(a);" in src, cols
+        # every candidate of a long row (4, 8 and 16 waves) has a template
+        for cols in (4096, 8192, 16384, 32768, 40000, 65536):
             e = row_entry(op, 64, cols)
             for cfg in rt.candidates(op, 64, cols, 0):
                 e["best"] = cfg
