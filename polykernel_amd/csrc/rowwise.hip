@@ -57,6 +57,17 @@ __global__ __launch_bounds__(kBlock) void softmax_generic_kernel(RowArgs a) {
   softmax_generic_body<MODE>(a);
 }
 
+// Rows of up to 131072 columns: 16 waves, the row as packed bf16 in registers.
+template <bool RESID>
+__global__ __launch_bounds__(kPackedLanes) void rmsnorm_packed_kernel(RowArgs a) {
+  rmsnorm_packed_body<RESID>(a);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kPackedLanes) void softmax_packed_kernel(RowArgs a) {
+  softmax_packed_body<MODE>(a);
+}
+
 // ---- configurations ---------------------------------------------------------
 // A row config: block_m = rows per workgroup (4: one wave per row; 1: one
 // row per workgroup of num_warps waves, 4, 8 or 16), block_n = cols, num_warps,
@@ -72,6 +83,8 @@ __global__ __launch_bounds__(kBlock) void softmax_generic_kernel(RowArgs a) {
 //   still fits in registers: measured at 32768 columns residual+RMSNorm 478 ->
 //   136 us and masked softmax 621 -> 184 us against the generic kernel, at
 //   65536 columns 491 -> 176 and 622 -> 238 us, [rows, cols] of 2^27 elements);
+//   8193 to 16384 vectors (up to 131072 columns): 16 waves, 16 vectors per
+//   lane as packed bf16 (num_warps 16, unroll 16);
 //   cols % 8 != 0 or longer rows: the generic kernel.
 int row_vpt(int nvec, int lanes) {
   for (int v : {1, 2, 4, 8, 16})
@@ -99,6 +112,9 @@ int row_configs(bool softmax, int rows, int cols, pk_config *out, int cap) {
     // vectors per lane first, 8 waves with 8 or 16 second
     c[n++] = pk_config{1, cols, 0, 16, 8, std::max(4, row_vpt(nvec, 1024)), 1};
     c[n++] = pk_config{1, cols, 0, 8, 8, std::max(8, row_vpt(nvec, 512)), 1};
+  } else if (cols % 8 == 0 && nvec <= kPackedLanes * kPackedVpt) {
+    // up to 131072 columns: 16 waves, 16 vectors per lane held as packed bf16
+    c[n++] = pk_config{1, cols, 0, kPackedWaves, 8, kPackedVpt, 1};
   } else {
     c[n++] = pk_config{1, cols, 0, 4, 1, 1, 1};
   }
@@ -147,6 +163,7 @@ int rmsnorm_run(const RowArgs &a, const pk_config &c, hipStream_t st) {
     switch (c.unroll) {
       case 4: rmsnorm_vec_kernel<16, 4, RESID><<<rows, 1024, 0, st>>>(a); return PK_OK;
       case 8: rmsnorm_vec_kernel<16, 8, RESID><<<rows, 1024, 0, st>>>(a); return PK_OK;
+      case 16: rmsnorm_packed_kernel<RESID><<<rows, kPackedLanes, 0, st>>>(a); return PK_OK;
     }
   }
   set_error("rmsnorm: config {%d, %d, %d, %d, %d, %d, %d} has no kernel", c.block_m, c.block_n, c.block_k,
@@ -186,6 +203,7 @@ int softmax_run(const RowArgs &a, const pk_config &c, hipStream_t st) {
     switch (c.unroll) {
       case 4: softmax_vec_kernel<16, 4, MODE><<<rows, 1024, 0, st>>>(a); return PK_OK;
       case 8: softmax_vec_kernel<16, 8, MODE><<<rows, 1024, 0, st>>>(a); return PK_OK;
+      case 16: softmax_packed_kernel<MODE><<<rows, kPackedLanes, 0, st>>>(a); return PK_OK;
     }
   }
   set_error("softmax: config {%d, %d, %d, %d, %d, %d, %d} has no kernel", c.block_m, c.block_n, c.block_k,

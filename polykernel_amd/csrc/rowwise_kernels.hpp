@@ -309,5 +309,128 @@ __device__ __forceinline__ void softmax_generic_body(const RowArgs &a) {
     y[base + c] = (uint16_t)f2bf(expf(load_z1<MODE>(in, mask, base + c) - m) * inv);
 }
 
+// ---------------------------------------------------------------------------
+// Rows of up to kPackedLanes * kPackedVpt * 8 = 131072 columns (cols % 8 == 0,
+// 16-byte aligned): one row per workgroup of 16 waves, each lane keeping its
+// 16 vectors as packed bf16 -- the values both ops hold are bf16 (the rounded
+// residual sum s, or x; the rounded masked logit z) -- so the row stays in 64
+// registers and HBM is read once.  Softmax evaluates exp(z - m) twice, for
+// the sum and for the output.  Arithmetic as in the vector bodies.
+// ---------------------------------------------------------------------------
+constexpr int kPackedWaves = 16, kPackedLanes = kPackedWaves * 64, kPackedVpt = 16;
+
+template <bool RESID>
+__device__ __forceinline__ void rmsnorm_packed_body(const RowArgs &a) {
+#pragma clang fp contract(off)
+  const uint16_t *__restrict__ x = static_cast<const uint16_t *>(a.in);
+  const uint16_t *__restrict__ r = a.aux;
+  const uint16_t *__restrict__ w = a.gamma;
+  uint16_t *__restrict__ y = a.out;
+  __shared__ float red[kPackedWaves];
+  const int lane = threadIdx.x;
+  const int nvec = a.cols >> 3;
+  const size_t base = (size_t)blockIdx.x * a.cols;
+  U4 pv[kPackedVpt];
+  float ss = 0.f;
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < kPackedVpt; ++i) {
+    const int c = lane + i * kPackedLanes;
+    if (c < nvec) {
+      U4 xw = ld16_once(x + base + (size_t)c * 8);
+      float v[8];
+      unpack8(xw, v);
+      if constexpr (RESID) {
+        float rv[8];
+        unpack8(ld16_once(r + base + (size_t)c * 8), rv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = bf2f(f2bf(v[e] + rv[e]));
+        xw = pack8(v);  // exact: the values are bf16
+      }
+      pv[i] = xw;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ss += v[e] * v[e];
+        ok &= div_elem_ok(v[e]);
+      }
+    }
+  }
+  ss = group_sum<kPackedWaves>(ss, red);
+  const float rms = sqrtf(ss * a.inv_cols + a.eps);
+  const bool fast = __all(ok && div_row_ok(rms));
+  const float rinv = 1.0f / rms;
+#pragma unroll
+  for (int i = 0; i < kPackedVpt; ++i) {
+    const int c = lane + i * kPackedLanes;
+    if (c < nvec) {
+      float v[8], o[8];
+      unpack8(pv[i], v);
+      if (fast) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = div_fast(v[e], rms, rinv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = v[e] / rms;
+      }
+      if (w) {
+        float g[8];
+        unpack8(ld16(w + (size_t)c * 8), g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] *= g[e];
+      }
+      st16(y + base + (size_t)c * 8, pack8(o));
+    }
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void softmax_packed_body(const RowArgs &a) {
+#pragma clang fp contract(off)
+  const void *__restrict__ in = a.in;
+  const uint16_t *__restrict__ mask = a.aux;
+  uint16_t *__restrict__ y = a.out;
+  __shared__ float red[kPackedWaves];
+  const int lane = threadIdx.x;
+  const int nvec = a.cols >> 3;
+  const size_t base = (size_t)blockIdx.x * a.cols;
+  U4 zp[kPackedVpt];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kPackedVpt; ++i) {
+    const int c = lane + i * kPackedLanes;
+    if (c < nvec) {
+      float z[8];
+      load_z8<MODE>(in, mask, base + (size_t)c * 8, z);
+      zp[i] = pack8(z);  // exact: z are bf16 values
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, z[e]);
+    }
+  }
+  m = group_max<kPackedWaves>(m, red);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPackedVpt; ++i) {
+    if (lane + i * kPackedLanes < nvec) {
+      float z[8];
+      unpack8(zp[i], z);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += expf(z[e] - m);
+    }
+  }
+  s = group_sum<kPackedWaves>(s, red);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int i = 0; i < kPackedVpt; ++i) {
+    const int c = lane + i * kPackedLanes;
+    if (c < nvec) {
+      float z[8], o[8];
+      unpack8(zp[i], z);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = expf(z[e] - m) * inv;
+      st16(y + base + (size_t)c * 8, pack8(o));
+    }
+  }
+}
+
 }  // namespace row
 }  // namespace pk

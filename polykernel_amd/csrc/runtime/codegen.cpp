@@ -128,7 +128,10 @@ bool RowInstance(const Config &c, bool softmax, const std::string &kind, std::st
   }
   if (c.block_m != 1 || (c.num_warps != 4 && c.num_warps != 8 && c.num_warps != 16) || c.unroll > 16) return false;
   threads = 64 * c.num_warps;
-  body = ns + "vec_body<" + std::to_string(c.num_warps) + ", " + std::to_string(c.unroll) + ", " + kind + ">";
+  if (c.num_warps == 16 && c.unroll == 16)  // rows held as packed bf16
+    body = ns + "packed_body<" + kind + ">";
+  else
+    body = ns + "vec_body<" + std::to_string(c.num_warps) + ", " + std::to_string(c.unroll) + ", " + kind + ">";
   return true;
 }
 

@@ -50,9 +50,10 @@ INT8_SHAPE = (24, 1040, 1024)
 ATT_SQ, ATT_SCACHE, ATT_HEAD_DIMS = 200, 256, (64, 128, 96, 256, 512, 300)
 # row ops: 37 rows (ragged for four rows per workgroup); the widths reach
 # every vector kernel (one wave per row with 1/2/4/8 vectors per lane, four
-# waves per row with 2/4/8, eight with 1/2/4/8/16, sixteen with 4/8) and the
-# generic kernel (cols % 8 != 0, or more than 65536 columns)
-ROW_ROWS, ROW_COLS = 37, (512, 1024, 2048, 4096, 8192, 16384, 32768, 65536, 70000, 1000, 999)
+# waves per row with 2/4/8, eight with 1/2/4/8/16, sixteen with 4/8 and the
+# packed-bf16 16x16) and the generic kernel (cols % 8 != 0, or more than
+# 131072 columns)
+ROW_ROWS, ROW_COLS = 37, (512, 1024, 2048, 4096, 8192, 16384, 32768, 65536, 70000, 131072, 140000, 1000, 999)
 # RMSNorm -> MatMul: the whole-K panel (ragged M), the double-buffered panel
 # and the long-row path (RMSNorm into workspace, then a GEMM)
 PANEL_SHAPES = ((40, 136, 768), (64, 256, 1536), (72, 264, 2048))

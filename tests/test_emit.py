@@ -97,7 +97,10 @@ def test_emit_source_row_templates():
                     f"pk::row::{body}<{nw}, {vpt}, {kind}>(a);") in src, (op, cols, src)
             assert f"void pk_row_any(pk_row_args a) {{\n  pk::row::{any_}(a);" in src, (op, cols)
             assert '#include "rowwise_kernels.hpp"' in src
-        for cols in (999, 70000):  # cols % 8 != 0, and rows longer than 65536 columns
+        for cols in (70000, 131072):  # 65537-131072 columns: the packed-bf16 kernel
+            src = rt.emit_source(row_entry(op, 64, cols))
+            assert f"__launch_bounds__(1024) void pk_row(pk_row_args a) {{\n  pk::row::{body.replace('vec', 'packed')}<{kind}>(a);" in src, cols
+        for cols in (999, 140000):  # cols % 8 != 0, and rows longer than 131072 columns
             src = rt.emit_source(row_entry(op, 64, cols))
             assert f"void pk_row(pk_row_args a) {{\n  pk::row::{any_}(a);" in src, cols
         # every candidate of a long row (4, 8 and 16 waves) has a template

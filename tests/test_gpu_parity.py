@@ -181,12 +181,13 @@ def test_softmax_mask(gpu, oracle, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols", [(37, 2048), (37, 4096), (37, 6000), (37, 8192), (21, 12000), (37, 16384),
-                                       (13, 32768), (5, 40000), (7, 65536), (3, 70000)])
+                                       (13, 32768), (5, 40000), (7, 65536), (3, 70000), (3, 128256), (2, 131072),
+                                       (2, 140000)])
 def test_row_ops_every_config(gpu, oracle, rows, cols):
     """Every candidate of residual + RMSNorm and masked softmax (one wave per
-    row, a workgroup of 4, 8 or 16 waves per row, the generic kernel past
-    65536 columns; ragged rows and widths that leave lanes idle) through
-    pk_*_config against the oracle."""
+    row, a workgroup of 4, 8 or 16 waves per row, the packed-bf16 kernel up to
+    131072 columns, the generic kernel past them; ragged rows and widths that
+    leave lanes idle) through pk_*_config against the oracle."""
     from polykernel_amd import runtime as rt
 
     x, r = synth.normal_bf16((rows, cols), 3), synth.normal_bf16((rows, cols), 4)
