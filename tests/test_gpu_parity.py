@@ -131,7 +131,7 @@ def test_gelu_all_bf16_codes_bit_exact(gpu, oracle):
 
 @pytest.mark.parametrize("rows,cols,gamma", [(2048, 4096, False), (128, 768, True), (7, 130, True),
                                              (64, 8192, True), (3, 16384, False), (5, 24, False),
-                                             (4, 20000, True)])
+                                             (4, 20000, True), (3, 65536, False), (2, 131072, True)])
 def test_rmsnorm(gpu, oracle, rows, cols, gamma):
     _say(f"rmsnorm {rows}x{cols} gamma={gamma}")
     x = synth.normal_bf16((rows, cols), 1)
@@ -153,7 +153,8 @@ def test_residual_rmsnorm(gpu, oracle, rows, cols):
     assert rep.bit_exact >= 0.99 and rep.max_ulp <= 1, rep
 
 
-@pytest.mark.parametrize("rows,cols", [(8, 16), (64, 1000), (128, 8192), (3, 2), (2, 20000)])
+@pytest.mark.parametrize("rows,cols", [(8, 16), (64, 1000), (128, 8192), (3, 2), (2, 20000), (3, 65536),
+                                       (2, 131072)])
 def test_softmax(gpu, oracle, rows, cols):
     _say(f"softmax {rows}x{cols}")
     x = rng_bf16((rows, cols), 6, -8, 8)
