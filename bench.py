@@ -151,16 +151,31 @@ class Timer:
         self.sp = self.stream.cuda_stream
         self.stats = {}
 
-    def __call__(self, fn, key=None, warm=3, flush=None):
+    def __call__(self, fn, key=None, warm=3, flush=None, warm_s=0.05):
         """Mean per launch over `reps` back-to-back launches (the median of
         three such batches; per-launch pairs of events when `flush` runs
         between launches); with `key`, the median and minimum of `reps`
-        launches timed one by one go into stats[key]."""
+        launches timed one by one go into stats[key].
+
+        Before timing, `warm` launches and then `warm_s` seconds of sustained
+        launches: the memory and fabric clocks fall within milliseconds of
+        idle and take ~15 ms of load to climb back (measured: the first 20-launch
+        batches of config 4a after setup ran 131-143 us per launch, later ones
+        124-126 us), and production code runs these kernels back to back."""
         import torch
 
         n, stream = self.reps, self.stream
         for _ in range(warm):
             fn()
+        if warm_s > 0 and flush is None:
+            e0, e1 = event_pair()
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            per_s = max(e0.elapsed_time(e1) * 1e-3, 1e-6)
+            for _ in range(min(int(warm_s / per_s) + 1, 20000)):
+                fn()
         evs = [event_pair() for _ in range(n)]
         for e0, e1 in evs:
             if flush is not None:
