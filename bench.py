@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: the config-2 fused MLP block on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 40]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 40] [--settle-ms 250]
 
 A step is one pass of the MLP block over the config-2 batch (BASELINE.json
 configs[1]): RMSNorm(x, gamma) -> MatMul W1 [4096,16384] + b1 -> GELU(erf) ->
@@ -13,7 +13,10 @@ gfx950 tuning cache (polykernel_amd/tuning/gfx950.json, written by the
 correctness-gated autotuner), with HIP events around the dominant GEMM launch
 on the stream it runs on.
 
-value = 2^40 algorithmic FLOP per step / wall time per step (TFLOP/s).
+value = 2^40 algorithmic FLOP per step / wall time per step (TFLOP/s), over
+exactly --steps timed steps after --warmup untimed ones, which follow
+--settle-ms of untimed steps (the clocks climb for ~50 steps after the idle
+input set-up).
 The other BASELINE configs (attention prefill, residual+RMSNorm, masked
 softmax, int8 decode, RMSNorm->MatMul) are reported under "extra", each with
 the CPU oracle timed on one thread and on all threads (a bounded sample,
@@ -64,7 +67,7 @@ def event_pair():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def bench_mlp(steps: int, warmup: int):
+def bench_mlp(steps: int, warmup: int, settle_ms: float = 250.0):
     import numpy as np
     import torch
 
@@ -110,9 +113,22 @@ def bench_mlp(steps: int, warmup: int):
         if ev is not None:
             ev[3].record(stream)
 
+    # Clock settle before the warmup steps: untimed steps for settle_ms of wall
+    # time.  After the idle input set-up the first ~50 steps run ~5-10 % slow
+    # while the clocks climb to their sustained state (0.98 ms per step measured
+    # with 5 warmups, 0.89-0.92 ms after 40 or more), so with few warmup steps the
+    # timed steps would sample that ramp rather than the block's sustained rate.
+    settle_steps = 0
+    t_end = time.perf_counter() + settle_ms * 1e-3
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            step()
+        settle_steps += 8
+        torch.cuda.synchronize()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    log(f"clock settle: {settle_steps} untimed steps in {settle_ms:.0f} ms, then {warmup} warmup steps")
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -136,7 +152,7 @@ def bench_mlp(steps: int, warmup: int):
     torch.cuda.synchronize()
     entry_ms = e0.elapsed_time(e1) / 3
     inputs = dict(x=x, g=g, w1=w1, b1=b1, w2=w2, b2=b2)
-    return elapsed, g1, g2, entry_ms, inputs, (entry1, entry2)
+    return elapsed, g1, g2, entry_ms, inputs, (entry1, entry2), settle_steps
 
 
 class Timer:
@@ -577,6 +593,8 @@ def main() -> int:
     # while the clocks settle (sustained: 0.89 ms/step over 600 steps)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--settle-ms", type=float, default=250.0,
+                    help="untimed MLP steps for this long before the warmup steps (clock settle; 0: none)")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
     ap.add_argument("--only", choices=sorted(EXTRA), default=None,
@@ -621,7 +639,7 @@ def main() -> int:
         res = bench_extra(cpu=not args.no_cpu, only=args.only)
         print(json.dumps({"only": args.only, "host": host_info(), **res}), flush=True)
         return 0
-    elapsed, g1, g2, entry_ms, inputs, entries = bench_mlp(args.steps, args.warmup)
+    elapsed, g1, g2, entry_ms, inputs, entries, settle_steps = bench_mlp(args.steps, args.warmup, args.settle_ms)
     ms_step = elapsed / args.steps * 1e3
     value = MLP_FLOP / (ms_step * 1e-3) / 1e12
     g1_ms = sum(g1) / len(g1)
@@ -636,6 +654,8 @@ def main() -> int:
         "gemm1_bias_gelu_ms": round(g1_ms, 4), "gemm2_bias_residual_ms": round(g2_ms, 4),
         "gemm2_tflops": round(GEMM_FLOP / (g2_ms * 1e-3) / 1e12, 1),
         "launch_mlp_block_ms": round(entry_ms, 4),
+        "clock_settle": {"ms": args.settle_ms, "untimed_steps": settle_steps,
+                         "note": "untimed steps before the warmup steps, so the timed steps see sustained clocks"},
         "served_configs": [entries[0]["best"], entries[1]["best"]],
         "frac_mfma_block": round(value / PEAK_BF16_TFLOPS, 4)}
     cpu = None
