@@ -400,7 +400,12 @@ __device__ __forceinline__ void softmax_packed_body(const RowArgs &a) {
   const int nvec = a.cols >> 3;
   const size_t base = (size_t)blockIdx.x * a.cols;
   U4 zp[kPackedReg];
-  float m = -INFINITY;
+  // Online sum while the row streams in: each lane keeps its running max ml and
+  // sl = sum exp(z - ml), rescaled by exp(ml_old - ml) when ml grows, so the
+  // exponentials of the sum overlap the loads and only the output pass
+  // evaluates them again.  A lane that has seen only -inf keeps ml = -inf and
+  // sl = 0.
+  float ml = -INFINITY, sl = 0.f;
 #pragma unroll
   for (int i = 0; i < kPackedVpt; ++i) {
     const int c = lane + i * kPackedLanes;
@@ -411,28 +416,28 @@ __device__ __forceinline__ void softmax_packed_body(const RowArgs &a) {
       // both branches of the unrolled loop)
       if (i < kPackedReg) zp[i < kPackedReg ? i : 0] = pack8(z);  // exact: z are bf16 values
       else zl[i - kPackedReg][lane] = pack8(z);
+      float cm = z[0];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, z[e]);
+      for (int e = 1; e < 8; ++e) cm = fmaxf(cm, z[e]);
+      const float mn = fmaxf(ml, cm);
+      if (mn != -INFINITY) {
+        float t = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t += expf(z[e] - mn);
+        sl = sl * expf(ml - mn) + t;
+        ml = mn;
+      }
     }
   }
-  m = group_max<kPackedWaves>(m, red);
+  const float m = group_max<kPackedWaves>(ml, red);
   auto chunk = [&](int i) __attribute__((always_inline)) -> U4 {
     return i < kPackedReg ? zp[i < kPackedReg ? i : 0] : zl[i - kPackedReg][lane];
   };
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < kPackedVpt; ++i) {
-    if (lane + i * kPackedLanes < nvec) {
-      float z[8];
-      unpack8(chunk(i), z);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += expf(z[e] - m);
-    }
-  }
   // an opaque lane: the output pass recomputes its store addresses instead of
   // keeping 16 of them live across the reductions
   asm volatile("" : "+v"(lane));
-  s = group_sum<kPackedWaves>(s, red);
+  // a row of -inf only: m = -inf and every output is NaN, as exp(-inf - -inf)
+  const float s = group_sum<kPackedWaves>(ml == -INFINITY ? 0.f : sl * expf(ml - m), red);
   const float inv = 1.0f / s;
 #pragma unroll
   for (int i = 0; i < kPackedVpt; ++i) {
