@@ -314,11 +314,13 @@ __device__ __forceinline__ void softmax_generic_body(const RowArgs &a) {
 // 16-byte aligned): one row per workgroup of 16 waves, each lane keeping its
 // 16 vectors as packed bf16 -- the values both ops hold are bf16 (the rounded
 // residual sum s, or x; the rounded masked logit z) -- so the row stays in 64
-// registers and HBM is read once.  Softmax evaluates exp(z - m) twice, for
-// the sum and for the output, and keeps half of its chunks in LDS (128 KiB)
-// so that the exponentials' temporaries fit the 128 registers of a 1024-thread
-// workgroup without spilling (vocabulary-length rows 2.9-3.4 -> 3.5-4.1 TB/s,
-// bit-identical).  Arithmetic as in the vector bodies.
+// registers and HBM is read once.  Softmax keeps half of its chunks in LDS
+// (128 KiB) so that the exponentials' temporaries fit the 128 registers of a
+// 1024-thread workgroup without spilling (vocabulary-length rows 2.9-3.4 ->
+// 3.5-4.1 TB/s, bit-identical), and sums online while the row arrives (each
+// lane's sum rescaled whenever its running max grows), so exp(z - m) is
+// evaluated again only for the output (4.3-4.9 TB/s).  RMSNorm arithmetic as
+// in the vector bodies.
 // ---------------------------------------------------------------------------
 constexpr int kPackedWaves = 16, kPackedLanes = kPackedWaves * 64, kPackedVpt = 16;
 
