@@ -212,6 +212,35 @@ def test_row_ops_every_config(gpu, oracle, rows, cols):
                 assert np.all(f32(got)[mask == 0xFF80] == 0.0)
 
 
+@pytest.mark.parametrize("cols", [1000, 8192, 65536, 131072])
+def test_softmax_mask_special_rows(gpu, oracle, cols):
+    """Rows the online and two-pass sums must treat as the oracle does, on every
+    config: all positions masked (max -inf: NaN everywhere), one position
+    unmasked (exactly 1 there, 0 elsewhere), a +inf logit (NaN everywhere), the
+    +inf in the last chunk after finite values, and an ordinary row."""
+    from polykernel_amd import runtime as rt
+
+    rows = 5
+    logits = synth.normal_f32((rows, cols), 21, 2.0)
+    mask = synth.mask_bf16((rows, cols), 22, 0.1)
+    mask[0, :] = 0xFF80
+    mask[1, :] = 0xFF80
+    mask[1, cols // 3] = 0
+    logits[2, 7] = np.inf
+    logits[3, cols - 1] = np.inf
+    want = oracle.softmax_mask(logits, mask)
+    wf = f32(want)
+    assert np.all(np.isnan(wf[[0, 2, 3]])) and wf[1, cols // 3] == 1.0
+    for cfg in rt.candidates("fused_softmax_mask", rows, cols, 0):
+        _say(f"softmax special rows {cols} {cfg}")
+        got = f32(from_dev(K().fused_softmax_mask(to_dev(logits), to_dev(mask), config=cfg)))
+        assert np.array_equal(np.isnan(got), np.isnan(wf)), cfg
+        assert np.array_equal(got[1], wf[1]), cfg
+        rep = mt.report(from_dev(K().fused_softmax_mask(to_dev(logits[4:]), to_dev(mask[4:]), config=cfg)),
+                        want[4:])
+        assert rep.cosine >= 0.999 and rep.bit_exact >= 0.98, (cfg, rep)
+
+
 def test_row_config_refusals(gpu):
     """A config outside the shape's list is an argument error; a vector config
     with operands that are not 16-byte aligned is refused (the built-in choice
