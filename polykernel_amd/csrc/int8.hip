@@ -289,11 +289,13 @@ bool i8s_shape_ok(int M, int N, int K) {
 // Relative streaming rate of a workgroup of `waves` waves that reads `run`
 // contiguous bytes per weight row, from measurements on MI355X with rotating
 // 256 MiB buffers: 512 B runs of 4 waves ~5.0 TB/s (the contiguous-read
-// ceiling is ~5.7), 256 B ~4.4, 128 B ~3.4; runs that are not a multiple of
-// the 128 B cache line lose ~15 % (lines shared by two CUs); 2 or 8 waves
-// per workgroup lose ~10 %.
+// ceiling is ~5.7), 128 B ~3.4; 256 B runs probed at ~4.4 but the kernel
+// itself streams them at 0.77-0.8 of its 512 B rate (M 16: [4096, 11008]
+// 20.1 us with 256-column units against 16.7 with 512, equal bytes per unit);
+// runs that are not a multiple of the 128 B cache line lose ~15 % (lines
+// shared by two CUs); 2 or 8 waves per workgroup lose ~10 %.
 double i8s_run_efficiency(int run, int waves) {
-  double e = run >= 512 ? 1.0 : run >= 256 ? 0.87 : run >= 128 ? 0.68 : run >= 64 ? 0.55 : 0.4;
+  double e = run >= 512 ? 1.0 : run >= 256 ? 0.8 : run >= 128 ? 0.68 : run >= 64 ? 0.55 : 0.4;
   if (run % 128 != 0) e *= 0.85;
   if (waves != 4) e *= 0.9;
   return e;
@@ -301,10 +303,14 @@ double i8s_run_efficiency(int run, int waves) {
 
 // Pick the variant and K split for a shape: every CU should stream the same
 // number of weight bytes once (units = slices * splits * m-blocks, close to a
-// multiple of the CU count), in runs of >= 256 B per row; splits cost their
-// fp32 partials (written and read back) plus a second launch (counted as
-// ~24 MB of HBM time).  Fields of `req` that are nonzero are honoured;
-// returns false when nothing matches.
+// multiple of the usable CU count), in runs of >= 256 B per row; splits cost
+// their fp32 partials (written and read back) plus a second launch (counted
+// as ~24 MB of HBM time).  Rounds are counted against 7/8 of the CUs: with
+// one unit per CU the launch behaves like two rounds (measured at M 16, 512
+// columns per unit: [8192, 8192] 23.9 us at 256 units, 23.5 at 304, 17.6 at
+// 192; [4096, 16384] 22.4 at 256, 19.5 at 208; [16384, 4096] 22.7 at 256,
+// 19.9 at 160), while 220-224 units stream at full rate.  Fields of `req`
+// that are nonzero are honoured; returns false when nothing matches.
 bool i8s_plan(int M, int N, int K, const pk_config *req, int cus, I8sPlan &best) {
   if (!i8s_shape_ok(M, N, K)) return false;
   const int ksteps = K / I8S_KSTEP;
@@ -338,7 +344,7 @@ bool i8s_plan(int M, int N, int K, const pk_config *req, int cus, I8sPlan &best)
       }
       const int splits = (ksteps + split_steps - 1) / split_steps;
       const double units = (double)slices * splits * mblocks;
-      const double rounds = std::ceil(units / cus);
+      const double rounds = std::ceil(units / std::max(1, cus * 7 / 8));
       const int run = std::min(nb, N);
       double cost = rounds * split_steps * I8S_KSTEP * (double)run * cus / i8s_run_efficiency(run, v.waves);
       if (splits > 1) cost += 2.0 * splits * M * (double)N * 4 + 24e6;
