@@ -66,13 +66,20 @@ int tile_grid_ok(int M, int N, int K, int bm, int bn, const char *name) {
   return PK_ERR_UNSUPPORTED;
 }
 
-template <int EPI>
-int gemm_dispatch(const GemmArgs &g, int tile, hipStream_t st) {
+// Whether tile 0 runs the direct-to-LDS 256x256 kernel for these operands
+// (otherwise the register-staged one).
+bool gemm_dma_fits(const GemmArgs &g) {
   const bool aligned = (g.K % 8 == 0) && (g.N % 8 == 0) && aligned16(g.A) && aligned16(g.B);
   const bool offsets32 = (size_t)g.K * g.N * 2 < (size_t(1) << 31) &&
                          (size_t)G2_BM * g.K * 2 < (size_t(1) << 31);
   const bool ep_aligned = aligned16(g.C) && (!g.R || aligned16(g.R)) && (!g.bias || aligned16(g.bias));
-  if (tile == 0 && aligned && ep_aligned && offsets32 && g.K % G2_BK == 0 && g.N >= 8) {
+  return aligned && ep_aligned && offsets32 && g.K % G2_BK == 0 && g.N >= 8;
+}
+
+template <int EPI>
+int gemm_dispatch(const GemmArgs &g, int tile, hipStream_t st) {
+  const bool aligned = (g.K % 8 == 0) && (g.N % 8 == 0) && aligned16(g.A) && aligned16(g.B);
+  if (tile == 0 && gemm_dma_fits(g)) {
     const int tiles = ((g.M + G2_BM - 1) / G2_BM) * ((g.N + G2_BN - 1) / G2_BN);
     gemm_dma_kernel<EPI, 5><<<tiles, G2_THREADS, 0, st>>>(g);
     PK_LAUNCH_CHECK("gemm_dma_kernel");
@@ -132,10 +139,18 @@ int gemm_launch_variant(const GemmArgs &g, int v, bool vec, hipStream_t st) {
 }
 
 // Largest tile that still gives at least ~one workgroup per CU.
-int pick_tile(int M, int N) {
+// With the direct-to-LDS kernel (`dma`), 256x256 from 72 tiles up: even one
+// round that leaves most CUs idle beats the 128x128 kernel's rounds (K 4096:
+// [1280, 4096] 80 tiles 69.5 against 73.0 us, [2048, 4096] 128 tiles 72.1
+// against 84.6, [3072, 3072] 144 tiles 73.4 against 137.0, [2048, 6144] 192
+// tiles 87.4 against 141.4), while at 64 tiles one full round of 128x128
+// tiles wins ([1024, 4096] 59.4 against 68.9 us).  The register-staged
+// 256x256 kernel keeps the 200-tile threshold; 64x64 below 200 128x128
+// tiles ([512, 4096] 41.4 against 57.4 us for 128x128).
+int pick_tile(int M, int N, bool dma) {
   const long t256 = (((long)M + 255) / 256) * (((long)N + 255) / 256);
   const long t128 = (((long)M + 127) / 128) * (((long)N + 127) / 128);
-  if (t256 >= 200) return 0;
+  if (t256 >= (dma ? 72 : 200)) return 0;
   if (t128 >= 200) return 1;
   return 2;
 }
@@ -162,9 +177,10 @@ int gemm_configs(int M, int N, int K, pk_config *out, int cap) {
 bool gemm_default(int M, int N, int K, pk_config *out) {
   if (M <= 0 || N <= 0 || K <= 0) return false;
   const int vw = (K % 8 == 0 && N % 8 == 0) ? 8 : 1;
-  const int tile = pick_tile(M, N);
+  const bool dma = vw == 8 && gemm_dma_shape_ok(N, K);
+  const int tile = pick_tile(M, N, dma);
   int v = tile == 0 ? GV_REG256 : tile == 1 ? GV_REG128 : GV_REG64;
-  if (tile == 0 && vw == 8 && gemm_dma_shape_ok(N, K)) v = GV_DMA5;
+  if (tile == 0 && dma) v = GV_DMA5;
   *out = gemm_variant_config(v, vw);
   return true;
 }
@@ -217,7 +233,7 @@ int gemm_run(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const u
     int rc = gelu_table(&g.gelu_tab);
     if (rc) return rc;
   }
-  if (tile < 0) tile = pick_tile(M, N);
+  if (tile < 0) tile = pick_tile(M, N, gemm_dma_fits(g));
   switch (epi) {
     case EPI_NONE: return gemm_dispatch<EPI_NONE>(g, tile, st);
     case EPI_BIAS_GELU: return gemm_dispatch<EPI_BIAS_GELU>(g, tile, st);
