@@ -76,9 +76,11 @@ __global__ __launch_bounds__(kPackedLanes) void softmax_packed_kernel(RowArgs a)
 // registers), block_k 0 and stages 1.  Candidates, the built-in choice first:
 //   short rows (RMSNorm <= 512 vectors of 8, softmax <= 256): one wave per row;
 //   longer rows up to 2048 vectors: a workgroup per row at 4 and at 8 waves
-//   (8 first for softmax and for RMSNorm rows above 1024 vectors -- measured
-//   on [16384, 8192]: masked softmax 168.9 -> 162.0 us, residual+RMSNorm equal;
-//   at 16384 columns 174.2 -> 171.8 and 136.5 -> 128.0 us);
+//   (8 first for softmax rows from 512 vectors and for RMSNorm rows above
+//   1024 -- measured on [16384, 8192]: masked softmax 168.9 -> 162.0 us,
+//   residual+RMSNorm equal; at 16384 columns 174.2 -> 171.8 and 136.5 ->
+//   128.0 us; softmax at 3072 columns takes 4 waves first, 164.6 against
+//   178.3 us);
 //   2049 to 8192 vectors (up to 65536 columns): 16 waves first, then 8 (the row
 //   still fits in registers: measured at 32768 columns residual+RMSNorm 478 ->
 //   136 us and masked softmax 621 -> 184 us against the generic kernel, at
@@ -104,7 +106,10 @@ int row_configs(bool softmax, int rows, int cols, pk_config *out, int cap) {
     // instantiations), 2 for softmax
     const pk_config w4{1, cols, 0, 4, 8, std::max(softmax ? 2 : 4, row_vpt(nvec, 256)), 1};
     const pk_config w8{1, cols, 0, 8, 8, std::max(softmax ? 1 : 2, row_vpt(nvec, 512)), 1};
-    const bool eight_first = softmax || nvec > 1024;
+    // 8 waves first above 1024 vectors, and for softmax from 512 (3072
+    // columns: 4 waves 164.6 against 178.3 us; 4096 a tie; 5120: 8 waves 164.2
+    // against 170.6 us; 2^27-element problems)
+    const bool eight_first = (softmax && nvec >= 512) || nvec > 1024;
     c[n++] = eight_first ? w8 : w4;
     c[n++] = eight_first ? w4 : w8;
   } else if (cols % 8 == 0 && nvec <= 8192) {
