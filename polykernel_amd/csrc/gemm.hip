@@ -242,10 +242,7 @@ int gemm_run(int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, const u
   }
 }
 
-// The RMSNorm -> MatMul panel kernels (bodies in gemm_kernels.hpp).
-__global__ __launch_bounds__(RP_WAVES * 64) void rmsnorm_panel_gemm_kernel(PanelArgs a) {
-  rmsnorm_panel_body(a);
-}
+// The RMSNorm -> MatMul panel kernel (body in gemm_kernels.hpp).
 __global__ __launch_bounds__(RQ_THREADS) void rmsnorm_panel_gemm_fast_kernel(PanelArgs a) {
   rmsnorm_panel_fast_body(a);
 }
@@ -253,19 +250,27 @@ __global__ __launch_bounds__(RQ_THREADS) void rmsnorm_panel_gemm_fast_kernel(Pan
 int rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, int rows, int cols,
                    float eps, hipStream_t st);
 
-// The kernel fused_rmsnorm_matmul runs for aligned operands, as a config:
-// whole-K panel kernel (x panel and W slice in LDS, 4 waves); double-buffered
-// panel kernel (2 waves, 64-deep k-tiles); otherwise row normalisation into
+// The whole-K panel kernel (x panel and W slice in LDS, 32 x 64 tiles) when K
+// <= 832 and its grid is one round of at most 256 tiles: a latency kernel
+// that reloads W for every 32 rows, so past one round RMSNorm into workspace
+// and the GEMM win (K 768: M 128 8.4 against 13.2 us; M 192 14.9 against 13.3;
+// M 1024 56.5 against 21.7; [4096, 4096] 215.8 against 36.5 us).  The
+// double-buffered panel kernel (2 waves, 64-deep k-tiles, K <= 1536) lost at
+// every measured shape (M 16-128, N 4096, K 1024: 25.9-34.9 against 14.0-15.2
+// us; [4096, 4096, 1024] 1152.6 against 43.0 us) and was removed.
+bool fast_panel_fits(int M, int N, int K) {
+  const long tiles = (((long)M + RQ_BM - 1) / RQ_BM) * (((long)N + RQ_BN - 1) / RQ_BN);
+  return K <= RQ_MAX_K && tiles <= 256 && (size_t)K * N * 2 < (size_t(1) << 31);
+}
+
+// The kernel fused_rmsnorm_matmul runs for aligned operands, as a config: the
+// whole-K panel kernel where fast_panel_fits, otherwise row normalisation into
 // workspace followed by the GEMM's own choice.
 bool rmsnorm_matmul_config(int M, int N, int K, pk_config *out) {
   if (M <= 0 || N <= 0 || K <= 0) return false;
-  const bool panel_ok = (K % BK == 0) && K <= RP_MAX_K && (N % 8 == 0);
-  if (panel_ok && K <= RQ_MAX_K && (size_t)K * N * 2 < (size_t(1) << 31)) {
+  const bool panel_ok = (K % BK == 0) && (N % 8 == 0);
+  if (panel_ok && fast_panel_fits(M, N, K)) {
     *out = pk_config{RQ_BM, RQ_BN, K, RQ_THREADS / 64, 8, K / 16, 1};
-    return true;
-  }
-  if (panel_ok) {
-    *out = pk_config{RP_BM, RP_BN, BK, RP_WAVES, 8, BK / 16, 2};
     return true;
   }
   return gemm_default(M, N, K, out);
@@ -276,11 +281,10 @@ int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_
   PK_CHECK_ARG(x && W && out, "%s: null tensor pointer", name);
   PK_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "%s: invalid shape M=%d N=%d K=%d", name, M, N, K);
   if (M == 0 || N == 0) return PK_OK;
-  static_assert(RQ_BM == RP_BM && RQ_BN == RP_BN, "both panel kernels use 32 x 64 output tiles");
-  if (int rc = tile_grid_ok(M, N, K, RP_BM, RP_BN, name)) return rc;
-  const bool panel_ok = (K % BK == 0) && K <= RP_MAX_K && (N % 8 == 0) && aligned16(x) &&
+  if (int rc = tile_grid_ok(M, N, K, RQ_BM, RQ_BN, name)) return rc;
+  const bool panel_ok = (K % BK == 0) && (N % 8 == 0) && aligned16(x) &&
                         aligned16(W) && (!gamma || aligned16(gamma));
-  if (panel_ok && K <= RQ_MAX_K && aligned16(out) && (size_t)K * N * 2 < (size_t(1) << 31)) {
+  if (panel_ok && fast_panel_fits(M, N, K) && aligned16(out)) {
     const int tiles = ((M + RQ_BM - 1) / RQ_BM) * ((N + RQ_BN - 1) / RQ_BN);
     const size_t lds = (size_t)K * 128 + (size_t)RQ_BM * K * 2;
     rmsnorm_panel_gemm_fast_kernel<<<tiles, RQ_THREADS, lds, st>>>(
@@ -288,15 +292,7 @@ int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_
     PK_LAUNCH_CHECK(name);
     return PK_OK;
   }
-  if (panel_ok) {
-    const int tiles = ((M + RP_BM - 1) / RP_BM) * ((N + RP_BN - 1) / RP_BN);
-    const size_t lds = (size_t)RP_BM * K * 2 + 2 * BK * RP_BN * 2;
-    rmsnorm_panel_gemm_kernel<<<tiles, RP_WAVES * 64, lds, st>>>(
-        PanelArgs{x, gamma, W, out, M, N, K, 1.0f / (float)K, eps});
-    PK_LAUNCH_CHECK(name);
-    return PK_OK;
-  }
-  // Long rows: normalise once into library workspace, then the plain GEMM.
+  // Otherwise: normalise once into library workspace, then the plain GEMM.
   WorkspaceLease lease;  // held until the GEMM that reads the panel is queued
   int rc = library_workspace((size_t)M * K * 2, st, lease);
   if (rc) return rc;

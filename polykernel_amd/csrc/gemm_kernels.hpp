@@ -712,144 +712,6 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// RMSNorm -> MatMul (fused_rmsnorm_matmul) with the normalised A row-panel resident in LDS
-// (short K: 32 x K bf16 <= 96 KiB).  The block first computes its 32 row RMS
-// values, writes bf16((x / rms) * gamma) into LDS once (exact fp32 division,
-// kernels/cpu/cpu_reference.cpp:16-44), then streams B k-tiles (double
-// buffered) through the same MFMA loop as gemm_kernel.
-// ---------------------------------------------------------------------------
-constexpr int RP_BM = 32, RP_BN = 64, RP_WAVES = 2;
-constexpr int RP_MAX_K = 1536;
-
-__device__ __forceinline__ void rmsnorm_panel_body(const PanelArgs &a) {
-#pragma clang fp contract(off)
-  const uint16_t *__restrict__ X = a.X;
-  const uint16_t *__restrict__ gamma = a.gamma;
-  const uint16_t *__restrict__ B = a.B;
-  uint16_t *__restrict__ C = a.C;
-  const int M = a.M, N = a.N, K = a.K;
-  const float inv_cols = a.inv_cols, eps = a.eps;
-  constexpr int NT = RP_WAVES * 64;
-  constexpr int BN = RP_BN;
-  constexpr int B_CHUNKS = BK * BN / 8, BC = B_CHUNKS / NT;
-  constexpr int BROW_CHUNKS = BN / 8;
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t *Ap = smem;                       // [32][K]
-  uint16_t *Bs0 = smem + RP_BM * K;          // [2][BK*BN]
-  __shared__ float rms_s[RP_BM];
-
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int tn = (N + BN - 1) / BN;
-  const int mt = blockIdx.x / tn, nt = blockIdx.x % tn;
-  const int m0 = mt * RP_BM, n0 = nt * BN;
-  const int kchunks = K >> 3;
-
-  // Row statistics: each wave reduces 16 rows.
-  for (int r = wid; r < RP_BM; r += RP_WAVES) {
-    const int gm = m0 + r;
-    float ss = 0.f;
-    if (gm < M) {
-      for (int c = lane; c < kchunks; c += 64) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a = lo_bf(v[e]), b = hi_bf(v[e]);
-          ss += a * a;
-          ss += b * b;
-        }
-      }
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) rms_s[r] = sqrtf(ss * inv_cols + eps);
-  }
-  __syncthreads();
-  // Normalise the panel into LDS (16-byte chunks swizzled by row within each
-  // aligned group of 8 chunks).
-  for (int q = tid; q < RP_BM * kchunks; q += NT) {
-    const int r = q / kchunks, c = q % kchunks;
-    const int gm = m0 + r;
-    u32x4 o = {0, 0, 0, 0};
-    if (gm < M) {
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
-      u32x4 gv = {0, 0, 0, 0};
-      if (gamma) gv = *reinterpret_cast<const u32x4 *>(gamma + c * 8);
-      const float rms = rms_s[r];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float a = lo_bf(v[e]) / rms, b = hi_bf(v[e]) / rms;
-        if (gamma) {
-          a *= lo_bf(gv[e]);
-          b *= hi_bf(gv[e]);
-        }
-        o[e] = pack_bf(a, b);
-      }
-    }
-    *reinterpret_cast<u32x4 *>(Ap + r * K + ((c ^ (r & 7)) << 3)) = o;
-  }
-
-  u32x4 rb[BC];
-  auto load_b = [&](int kt) {
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int i = 0; i < BC; ++i) {
-      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
-      const int gk = k0 + row, gn = n0 + c * 8;
-      rb[i] = (gk < K && gn < N) ? *reinterpret_cast<const u32x4 *>(B + (size_t)gk * N + gn)
-                                 : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto store_b = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < BC; ++i) {
-      const int q = tid + i * NT, row = q / BROW_CHUNKS, c = q % BROW_CHUNKS;
-      *reinterpret_cast<u32x4 *>(&Bs0[s * BK * BN + row * BN + ((c ^ swz_b<BN>(row)) << 3)]) = rb[i];
-    }
-  };
-
-  f32x16 acc;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-  const int KT = K / BK;
-  const int grp = lane >> 4, gi = lane & 15;
-  const int b_krow = 8 * (grp >> 1) + (gi >> 2);
-  const int b_col = wid * 32 + 16 * (grp & 1) + 4 * (gi & 3);
-  const int a_row = lane & 31;
-
-  load_b(0);
-  store_b(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) load_b(kt + 1);
-    const uint16_t *bs = Bs0 + cur * BK * BN;
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      const int c = kt * 8 + 2 * s + (lane >> 5);
-      const bf16x8 af = lds_read_a(Ap + a_row * K + ((c ^ (a_row & 7)) << 3));
-      i16x4 h[2];
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int k = 16 * s + 4 * r + b_krow;
-        const int cc = b_col >> 3;
-        h[r] = lds_read_tr(bs + k * BN + ((cc ^ swz_b<BN>(k)) << 3) + (b_col & 7));
-      }
-      short tmp[8] = {h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8, tmp), acc, 0,
-                                                     0, 0);
-    }
-    if (kt + 1 < KT) store_b(cur ^ 1);
-    __syncthreads();
-  }
-  const int n = n0 + wid * 32 + (lane & 31);
-  if (n < N) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = m0 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-      if (m < M) C[(size_t)m * N + n] = (uint16_t)f2bf(acc[i]);
-    }
-  }
-}
 
 // Latency-oriented RMSNorm -> MatMul for short rows (K <= 832, the config-1
 // fragment: a few MB, cache-resident, so one memory round trip dominates).

@@ -222,12 +222,6 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
                "  pk::gk::rmsnorm_panel_fast_body(a);\n}\n";
       return true;
     }
-    if (c.num_warps == 2) {  // double-buffered panel kernel
-      source = head + "#include \"gemm_kernels.hpp\"\n\n" +
-               "extern \"C\" __global__ __launch_bounds__(128) void pk_panel(pk_panel_args a) {\n"
-               "  pk::gk::rmsnorm_panel_body(a);\n}\n";
-      return true;
-    }
     // rows too long for a panel: RMSNorm (with gamma) at the (M, K) row
     // config into workspace, then the config's GEMM
     pk_config rc{};

@@ -66,10 +66,8 @@ long long ConfigSpace::LdsBytes(std::string_view op, const Shape &shape, const C
       return (long long)c.shared_memory_stages * c.num_warps * 1024LL * (nt + 2 * mt);
     }
     case Family::RmsnormMatmul:
-      // whole-K kernel: W slice (K x 64) + normalised panel (32 x K); panel
-      // kernel: the panel + a double-buffered 64 x 64 W tile
+      // whole-K kernel: W slice (K x 64) + normalised panel (32 x K)
       if (c.block_k == shape.k) return shape.k * 128LL + (long long)c.block_m * shape.k * 2;
-      if (c.num_warps == 2) return (long long)c.block_m * shape.k * 2 + 2LL * c.block_k * c.block_n * 2;
       return 2LL * c.shared_memory_stages * ((long long)c.block_m * c.block_k + (long long)c.block_k * c.block_n);
     case Family::Attention:
       // K/V ring + the query-group merge buffer it aliases

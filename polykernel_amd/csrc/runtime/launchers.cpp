@@ -323,7 +323,7 @@ LaunchFn CodeObjectRowLauncher(bool softmax, std::shared_ptr<ModuleTable> table)
   };
 }
 
-// RMSNorm -> MatMul code objects.  Panel configs (pk_panel): the operand
+// RMSNorm -> MatMul code objects.  The panel config (pk_panel): the operand
 // conditions and the LDS size of gemm.hip fused_rmsnorm_matmul for that
 // kernel.  A GEMM config: RMSNorm into library workspace (pk_row /
 // pk_row_any at the (M, K) row config), then pk_gemm with that config's
@@ -338,12 +338,10 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
     }
     if (!CheckEntry(e, p->M, p->N, p->K, error)) return false;
     const Config &c = e.best;
-    const bool fast = c.block_k == p->K && c.num_warps == 4, dbuf = c.num_warps == 2;
-    if (fast || dbuf) {
-      if (!Aligned16(p->x) || !Aligned16(p->W) || (p->gamma && !Aligned16(p->gamma)) ||
-          (fast && !Aligned16(p->out))) {
+    if (c.block_k == p->K && c.num_warps == 4) {
+      if (!Aligned16(p->x) || !Aligned16(p->W) || (p->gamma && !Aligned16(p->gamma)) || !Aligned16(p->out)) {
         error = "code-object RMSNorm -> MatMul panel config {" + autotune::ToString(c) +
-                "} needs 16-byte aligned x, W, gamma" + (fast ? " and out" : "");
+                "} needs 16-byte aligned x, W, gamma and out";
         return false;
       }
       const std::optional<CachedBinary> bin = BinaryOf(*table, e, error);
@@ -353,8 +351,8 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
       pk_panel_args a{p->x, p->gamma, p->W, p->out, p->M, p->N, p->K, 1.0f / (float)p->K, p->eps};
       unsigned tiles = 0;
       if (!TileGrid(p->M, p->N, p->K, 32, 64, tiles, error)) return false;
-      const unsigned lds = fast ? (unsigned)(p->K * 128 + 32 * p->K * 2) : (unsigned)(32 * p->K * 2 + 2 * 64 * 64 * 2);
-      return ModuleLaunch(mod->fns[0], tiles, 1, fast ? 256u : 128u, p->stream, a, "pk_panel", error, lds);
+      const unsigned lds = (unsigned)(p->K * 128 + 32 * p->K * 2);
+      return ModuleLaunch(mod->fns[0], tiles, 1, 256u, p->stream, a, "pk_panel", error, lds);
     }
     // GEMM config: the row normalisation, then the plain GEMM
     const bool dma = c.block_k == 32;

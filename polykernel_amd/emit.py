@@ -54,8 +54,8 @@ ATT_SQ, ATT_SCACHE, ATT_HEAD_DIMS = 200, 256, (64, 128, 96, 256, 512, 300)
 # packed-bf16 16x16) and the generic kernel (cols % 8 != 0, or more than
 # 131072 columns)
 ROW_ROWS, ROW_COLS = 37, (512, 1024, 2048, 4096, 8192, 16384, 32768, 65536, 70000, 131072, 140000, 1000, 999)
-# RMSNorm -> MatMul: the whole-K panel (ragged M), the double-buffered panel
-# and the long-row path (RMSNorm into workspace, then a GEMM)
+# RMSNorm -> MatMul: the whole-K panel (ragged M) and the RMSNorm-into-
+# workspace path followed by a GEMM (K 1536 and 2048)
 PANEL_SHAPES = ((40, 136, 768), (64, 256, 1536), (72, 264, 2048))
 
 

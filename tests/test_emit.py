@@ -113,13 +113,13 @@ def test_emit_source_row_templates():
 
 
 def test_emit_source_rmsnorm_matmul_templates():
-    """fused_rmsnorm_matmul: the whole-K panel (K <= 832), the double-buffered
-    panel (K <= 1536) and, for longer rows, RMSNorm at the (M, K) row config
-    followed by the config's GEMM."""
+    """fused_rmsnorm_matmul: the whole-K panel (K <= 832, one round of tiles)
+    and, otherwise, RMSNorm at the (M, K) row config followed by the config's
+    GEMM."""
     src = rt.emit_source(gemm_entry("fused_rmsnorm_matmul", 128, 3072, 768))
     assert "__launch_bounds__(256) void pk_panel(pk_panel_args a) {\n  pk::gk::rmsnorm_panel_fast_body(a);" in src
-    src = rt.emit_source(gemm_entry("fused_rmsnorm_matmul", 64, 256, 1536))
-    assert "__launch_bounds__(128) void pk_panel(pk_panel_args a) {\n  pk::gk::rmsnorm_panel_body(a);" in src
+    # past one round of panel tiles (M 300, N 4096): RMSNorm into workspace and the GEMM
+    assert "pk_panel" not in rt.emit_source(gemm_entry("fused_rmsnorm_matmul", 300, 4096, 768))
     e = gemm_entry("fused_rmsnorm_matmul", 72, 264, 2048)
     src = rt.emit_source(e)
     assert "pk::row::rmsnorm_vec_body<1, 4, false>(a);" in src and "rmsnorm_generic_body<false>(a);" in src

@@ -379,10 +379,10 @@ def test_fused_rmsnorm_matmul_config1(gpu, oracle):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(64, 128, 64), (130, 200, 1600), (40, 96, 2048), (130, 200, 832),
-                                    (33, 72, 128), (40, 96, 1024)])
+                                    (33, 72, 128), (40, 96, 1024), (128, 4096, 768), (300, 4096, 768)])
 def test_fused_rmsnorm_matmul_no_gamma(gpu, oracle, M, N, Kd):
-    """K <= 832: the latency-oriented kernel (ragged M and N); K <= 1536: the
-    panel kernel; longer rows: RMSNorm into workspace, then the GEMM."""
+    """K <= 832 and one round of 32 x 64 tiles: the latency-oriented panel
+    kernel (ragged M and N); otherwise RMSNorm into workspace, then the GEMM."""
     x = synth.normal_bf16((M, Kd), 24)
     w = synth.normal_bf16((Kd, N), 25, 1.0 / np.sqrt(Kd))
     got = from_dev(K().fused_rmsnorm_matmul(to_dev(x), to_dev(w), None, 1e-5))
