@@ -38,10 +38,9 @@
 //                                  generic kernel (grid rows, 256 threads)
 //     pk_row_any(pk_row_args)      the generic kernel, for operands the vector kernel cannot take
 //   fused_rmsnorm_matmul (gemm_kernels.hpp, rowwise_kernels.hpp):
-//     pk_panel(pk_panel_args)      block_k = K: the whole-K panel kernel (256 threads); num_warps 2:
-//                                  the double-buffered panel kernel (128 threads); grid
+//     pk_panel(pk_panel_args)      block_k = K: the whole-K panel kernel (256 threads); grid
 //                                  ceil(M/32) * ceil(N/64), dynamic LDS as in gemm.hip
-//   or, for a GEMM config (rows too long for a panel): the row normalisation into workspace
+//   or, for a GEMM config (every other shape): the row normalisation into workspace
 //     pk_row / pk_row_any(pk_row_args) (RMSNorm with gamma at the (M, K) row config), then
 //     pk_gemm(pk_gemm_args)        the config's GEMM kernel
 #include <fcntl.h>
