@@ -314,7 +314,12 @@ double i8s_run_efficiency(int run, int waves) {
 bool i8s_plan(int M, int N, int K, const pk_config *req, int cus, I8sPlan &best) {
   if (!i8s_shape_ok(M, N, K)) return false;
   const int ksteps = K / I8S_KSTEP;
-  int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  // rows per block: 16 up to M 16, 32 up to M 64 (two blocks at M 64: the
+  // 64-row variant holds only two ring stages; measured M 64 [8192, 28672]
+  // 66.1 against 71.3 us, [4096, 14336] 28.6 against 31.2), 64 above.  At
+  // M 32 two 16-row blocks lose once the weights outgrow the MALL (the
+  // second block re-reads them from HBM: [28672, 8192] 60.8 against 48.7 us)
+  int mt = M <= 16 ? 1 : M <= 64 ? 2 : 4;
   if (req && req->block_m) {
     if (req->block_m != 16 && req->block_m != 32 && req->block_m != 64) return false;
     mt = req->block_m / 16;

@@ -108,7 +108,7 @@ def test_noalloc_refuses_shapes_beyond_the_scratch(gpu):
     from polykernel_amd import _lib
 
     lib = _lib.load()
-    M, N, Kd = 64, 28672, 8192
+    M, N, Kd = 128, 28672, 8192
     need = _split_bytes(M, N, Kd)
     assert need is not None and need > SCRATCH_BYTES, need
     # plausible non-null pointers: the call must fail before any launch
