@@ -318,8 +318,11 @@ bool i8s_plan(int M, int N, int K, const pk_config *req, int cus, I8sPlan &best)
   // 64-row variant holds only two ring stages; measured M 64 [8192, 28672]
   // 66.1 against 71.3 us, [4096, 14336] 28.6 against 31.2), 64 above.  At
   // M 32 two 16-row blocks lose once the weights outgrow the MALL (the
-  // second block re-reads them from HBM: [28672, 8192] 60.8 against 48.7 us)
+  // second block re-reads them from HBM: [28672, 8192] 60.8 against 48.7 us),
+  // so they are taken only for weights of at most 128 MiB (half the MALL:
+  // [14336, 4096] 22.9 against 25.2 us, [4096, 14336] 23.4 against 26.5)
   int mt = M <= 16 ? 1 : M <= 64 ? 2 : 4;
+  if (M <= 32 && (size_t)K * N <= (size_t(128) << 20)) mt = 1;
   if (req && req->block_m) {
     if (req->block_m != 16 && req->block_m != 32 && req->block_m != 64) return false;
     mt = req->block_m / 16;
