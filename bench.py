@@ -138,6 +138,7 @@ def bench_mlp(steps: int, warmup: int, settle_ms: float = 250.0):
     elapsed = time.perf_counter() - t0
     g1 = [e[0].elapsed_time(e[1]) for e in evs]
     g2 = [e[2].elapsed_time(e[3]) for e in evs]
+    y_host = from_dev_bits(y)  # the served path's output, for the parity sample
 
     # the library's plain entry point (its built-in configs) on the same
     # buffers: equal work, reported beside the served path
@@ -151,7 +152,8 @@ def bench_mlp(steps: int, warmup: int, settle_ms: float = 250.0):
     e1.record(stream)
     torch.cuda.synchronize()
     entry_ms = e0.elapsed_time(e1) / 3
-    inputs = dict(x=x, g=g, w1=w1, b1=b1, w2=w2, b2=b2)
+    inputs = dict(x=x, g=g, w1=w1, b1=b1, w2=w2, b2=b2, y_gpu=y_host,
+                  entry_equal=bool(np.array_equal(from_dev_bits(y), y_host)))
     return elapsed, g1, g2, entry_ms, inputs, (entry1, entry2), settle_steps
 
 
@@ -298,6 +300,9 @@ def from_dev_bits(t):
     return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
 
 
+CFG1_BYTES = 5703168   # x 196,608 + gamma 1,536 + W 4,718,592 + out 786,432
+
+
 def bench_cfg1(t: Timer, cpu: bool) -> dict:
     """Config 1: RMSNorm -> MatMul fragment (cache-resident), warm and cold."""
     import torch
@@ -316,10 +321,26 @@ def bench_cfg1(t: Timer, cpu: bool) -> dict:
     ms = t(run, key="warm")
     big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
     ms_cold = t(run, key="cold", flush=lambda: big.fill_(1))
+    # the fixed cost of a launch of the panel kernel's geometry (192 workgroups
+    # of 256 threads, 144 KiB of dynamic LDS), timed the same way
+    tiles, lds = (128 // 32) * (3072 // 64), 768 * 128 + 32 * 768 * 2
+    floor = lambda: check(lib.pk_probe_empty_launch(tiles, 256, lds, t.sp), "empty launch")
+    ms_floor = t(floor, key="floor")
     flop = 2 * 128 * 3072 * 768
+    roof_us = CFG1_BYTES / (PEAK_HBM_GBS * 1e9) * 1e6
+
+    def roof(ms_):
+        gbs = CFG1_BYTES / (ms_ * 1e-3) / 1e9
+        return {"achieved": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
     out = {"us": round(ms * 1e3, 2), "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
            "warm": t.stats["warm"], "cold_us": round(ms_cold * 1e3, 2), "cold": t.stats["cold"],
-           "note": "warm: L2/MALL-resident (5.7 MB); cold: a 1 GiB buffer written between launches"}
+           "roofline": {"bound": "hbm", "unit": "GB/s", "peak": PEAK_HBM_GBS, "bytes": CFG1_BYTES,
+                        "time_at_peak_us": round(roof_us, 3), "warm": roof(ms), "cold": roof(ms_cold),
+                        "mfma_time_at_peak_us": round(flop / (PEAK_BF16_TFLOPS * 1e12) * 1e6, 3)},
+           "launch_floor_us": round(ms_floor * 1e3, 2), "launch_floor": t.stats["floor"],
+           "note": "warm: L2/MALL-resident (5.7 MB); cold: a 1 GiB buffer written between launches; "
+                   "launch_floor: an empty kernel with the panel kernel's grid, workgroup and LDS"}
     del big
     if cpu:
         from oracle import pyoracle
@@ -361,12 +382,21 @@ def bench_cfg3(t: Timer, cpu: bool) -> dict:
     kc[:, :, :Sc] = dev_bf16(h["kc"])
     vc[:, :, :Sc] = dev_bf16(h["vc"])
     o = torch.empty_like(q)
-    ms = t(lambda: check(lib.launch_fused_kv_append_attention(
+    run = lambda: check(lib.launch_fused_kv_append_attention(
         q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kn.data_ptr(), vn.data_ptr(), o.data_ptr(),
-        B, H, Sn, Sc, Dh, Sc + Sn, scale, 1, t.sp), "cfg3"), key="cfg3")
+        B, H, Sn, Sc, Dh, Sc + Sn, scale, 1, t.sp), "cfg3")
+    ms = t(run, key="cfg3")
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    ms_cold = t(run, key="cfg3_cold", flush=lambda: big.fill_(1))
+    del big
     tf = CFG3_FLOP / (ms * 1e-3) / 1e12
+    tf_cold = CFG3_FLOP / (ms_cold * 1e-3) / 1e12
     out = {"us": round(ms * 1e3, 2), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4),
-           **t.stats["cfg3"]}
+           **t.stats["cfg3"],
+           "cold_us": round(ms_cold * 1e3, 2), "tflops_cold": round(tf_cold, 2),
+           "frac_mfma_cold": round(tf_cold / PEAK_BF16_TFLOPS, 4), "cold": t.stats["cfg3_cold"],
+           "note": "us/tflops: back-to-back launches, the 84 MB of Q/K/V/O stay resident in the 256 MB MALL "
+                   "(cache-resident); cold: a 1 GiB buffer written before each launch (MALL flushed)"}
     if cpu:
         from oracle import pyoracle
 
@@ -537,20 +567,22 @@ def cpu_baseline(inputs, budget_s: float = 12.0):
     x = inputs["x"]
     rows = 16
     t0 = time.perf_counter()
-    pyoracle.mlp_block(x[:rows], inputs["g"], inputs["w1"], inputs["b1"], inputs["w2"], inputs["b2"], 1e-6)
+    outs = [pyoracle.mlp_block(x[:rows], inputs["g"], inputs["w1"], inputs["b1"], inputs["w2"], inputs["b2"],
+                               1e-6)]
     dt = time.perf_counter() - t0
     more = int(max(0, min(M - rows, rows * (budget_s / max(dt, 1e-3) - 1))))
     more = (more // 16) * 16
     if more > 0:
         t1 = time.perf_counter()
-        pyoracle.mlp_block(x[rows:rows + more], inputs["g"], inputs["w1"], inputs["b1"], inputs["w2"],
-                           inputs["b2"], 1e-6)
+        outs.append(pyoracle.mlp_block(x[rows:rows + more], inputs["g"], inputs["w1"], inputs["b1"],
+                                       inputs["w2"], inputs["b2"], 1e-6))
         dt += time.perf_counter() - t1
         rows += more
     flop = rows * 2 * (D * F + F * D)
-    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{rows} of {M} rows of the config-2 MLP block (rows are independent) in "
-                      f"{dt:.1f}s; oracle/oracle.c -O2 -ffp-contract=off, OpenMP over rows"}
+    res = {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "sample": f"{rows} of {M} rows of the config-2 MLP block (rows are independent) in "
+                     f"{dt:.1f}s; oracle/oracle.c -O2 -ffp-contract=off, OpenMP over rows"}
+    return res, np.concatenate(outs, axis=0)
 
 
 def cpu_baseline_single(inputs, rows: int = 16):
@@ -658,11 +690,16 @@ def main() -> int:
                          "note": "untimed steps before the warmup steps, so the timed steps see sustained clocks"},
         "served_configs": [entries[0]["best"], entries[1]["best"]],
         "frac_mfma_block": round(value / PEAK_BF16_TFLOPS, 4)}
+    extra["mlp_block_breakdown"]["launch_mlp_block_bits_equal_served"] = inputs["entry_equal"]
     cpu = None
+    parity = None
     if not args.no_cpu:
-        cpu = cpu_baseline(inputs)
+        cpu, want = cpu_baseline(inputs)
         cpu["cpu_model"] = extra["host"]["cpu_model"]
         log(f"cpu baseline: {cpu}")
+        parity = {**_parity(inputs["y_gpu"][:want.shape[0]], want),
+                  "rows": f"0..{want.shape[0] - 1} of {M} (the cpu_baseline sample)"}
+        log(f"parity sample: {parity}")
         extra["cpu_baseline_single_thread"] = cpu_baseline_single(inputs)
         log(f"cpu baseline, one thread: {extra['cpu_baseline_single_thread']}")
     line = {
@@ -672,6 +709,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_steps": settle_steps,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -687,6 +726,7 @@ def main() -> int:
                      "kernel": f"gemm_dma_kernel<EPI_BIAS_GELU,{entries[0]['best']['shared_memory_stages']},"
                                f"{entries[0]['best']['num_warps']},4> (GEMM1: x@W1+b1->GELU, 2^39 FLOP/launch)"},
         "cpu_baseline": cpu,
+        "parity_sample": parity,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

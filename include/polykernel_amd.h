@@ -94,8 +94,10 @@ PK_API int launch_softmax(const uint16_t *input, uint16_t *output, int rows, int
 
 /* out = matmul(rmsnorm(input, eps), weight), no gamma.
  * Replaces launch_fused_rmsnorm_matmul, kernels/generated/fused_rmsnorm_matmul.cu:114-116.
- * The normalised 32-row panel stays in LDS when K % 64 == 0 and K <= 1536;
- * otherwise it is staged once in library workspace. */
+ * The normalised 32-row panel stays in LDS (the whole-K panel kernel) when
+ * K % 64 == 0, K <= 832, N % 8 == 0, the operands are 16-byte aligned and the
+ * grid is one round of at most 256 tiles of 32 x 64; otherwise the rows are
+ * normalised once into library workspace and the GEMM reads them. */
 PK_API int launch_fused_rmsnorm_matmul(const uint16_t *input, const uint16_t *weight, uint16_t *output,
                                 int M, int N, int K, float eps, void *stream);
 
@@ -296,17 +298,36 @@ PK_API int pk_fused_softmax_mask_config(const float *logits, const uint16_t *mas
  * Mirrors the `neg` mode of lib/Runtime/hip_run_main.cpp:278-309. */
 PK_API int pk_probe_invalid_launch(int *launch_status, int *sync_status);
 
+/* Launch-floor probe: an empty kernel (no memory access) with `blocks`
+ * workgroups of `threads` threads and `lds_bytes` of dynamic LDS on `stream`,
+ * so a benchmark can time the fixed cost of a launch of a latency-bound
+ * kernel's geometry beside it.  No reference counterpart (a measurement aid
+ * like benchmarks/bench_hip.cpp's timing loop). */
+PK_API int pk_probe_empty_launch(int blocks, int threads, int lds_bytes, void *stream);
+
 /* ---- code-object support ----------------------------------------------------- */
 /* What a host needs to launch the emitted code objects: the device GELU table
  * of the current device (built on first use) and the library-owned workspace
  * of (current device, stream): a buffer of at least `bytes` for launches on
  * `stream` (hipStream_t; NULL = the null stream), grown on demand without a
- * device synchronisation, kept until the process ends.  Each stream has its
- * own buffer, so launches on different streams never share scratch; threads
+ * device synchronisation, kept until pk_release_workspace(stream) or the end
+ * of the process.  Each stream has its own buffer (hipStreamPerThread one per
+ * host thread), so launches on different streams never share scratch; threads
  * that feed ONE stream must serialise their launch sequences themselves (the
  * library's own entry points hold the slot's lock while they enqueue). */
 PK_API int pk_gelu_table(const uint16_t **table);
 PK_API int pk_library_workspace(size_t bytes, void *stream, void **ptr);
+
+/* Frees the library-owned workspace of (current device, stream) -- the
+ * buffer the split-K / split-KV / long-row RMSNorm->MatMul paths and
+ * pk_library_workspace use, and the smaller buffers it outgrew -- after
+ * hipStreamSynchronize(stream), so no queued kernel still reads it.  Call it
+ * before destroying a stream the library has run on (a new stream can reuse
+ * the old handle value) or to return the memory; the next call on the stream
+ * allocates again.  With hipStreamPerThread it frees the calling thread's
+ * buffer.  PK_OK if the stream has none.  No reference counterpart (its
+ * launchers own no memory, kernels/template/kernel_common.h). */
+PK_API int pk_release_workspace(void *stream);
 
 /* ---- naive device goldens (the autotuner's correctness gate) --------------- */
 /* Straightforward one-thread-per-output kernels that restate the reference

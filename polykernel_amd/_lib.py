@@ -126,7 +126,9 @@ SIGNATURES = {
     "pk_emit_code_object": (I, [P, C.c_char_p, C.c_char_p, C.c_char_p]),
     "pk_gelu_table": (I, [C.POINTER(P)]),
     "pk_probe_invalid_launch": (I, [C.POINTER(I), C.POINTER(I)]),
+    "pk_probe_empty_launch": (I, [I, I, I, P]),
     "pk_library_workspace": (I, [SZ, P, C.POINTER(P)]),
+    "pk_release_workspace": (I, [P]),
     "pk_runtime_destroy": (None, [P]),
     "pk_runtime_resolve": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p]),
     "pk_runtime_run": (I, [P, C.c_char_p, LL, LL, LL, C.c_char_p, P]),

@@ -4,9 +4,12 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstring>
+#include <functional>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <thread>
+#include <tuple>
 #include <vector>
 
 #include "pk_common.hpp"
@@ -21,16 +24,27 @@ std::mutex g_mu;
 bool g_table_ready[kMaxDevices] = {};
 const uint16_t *g_table_ptr[kMaxDevices] = {};
 
-// One workspace slot per (device, stream); slots live until the process ends
-// (their addresses stay valid for leases), buffers a slot outgrew stay
-// allocated beside it (`retired`).
+// One workspace slot per (device, stream); buffers a slot outgrew stay
+// allocated beside it (`retired`) until pk_release_workspace frees the slot
+// (or the process ends).  hipStreamPerThread names a different stream on
+// every host thread, so its slots are keyed by thread as well.  Leases hold a
+// reference, so a slot released while another thread waits for it stays
+// valid; that thread then sees `released` and takes the new slot.
 struct WsSlot {
   std::mutex mu;
   void *ptr = nullptr;
   size_t bytes = 0;
   std::vector<void *> retired;
+  bool released = false;
 };
-std::map<std::pair<int, uintptr_t>, WsSlot *> g_ws_slots;  // guarded by g_mu
+using WsKey = std::tuple<int, uintptr_t, size_t>;
+std::map<WsKey, std::shared_ptr<WsSlot>> g_ws_slots;  // guarded by g_mu
+
+WsKey ws_key(int dev, void *st) {
+  const size_t thread_tag =
+      st == (void *)hipStreamPerThread ? std::hash<std::thread::id>{}(std::this_thread::get_id()) : 0;
+  return WsKey{dev, reinterpret_cast<uintptr_t>(st), thread_tag};
+}
 }  // namespace
 
 void set_error(const char *fmt, ...) {
@@ -131,14 +145,20 @@ int library_workspace(size_t bytes, void *st, WorkspaceLease &lease) {
     set_error("device ordinal %d out of range", dev);
     return PK_ERR_UNSUPPORTED;
   }
-  WsSlot *slot;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    WsSlot *&s = g_ws_slots[{dev, reinterpret_cast<uintptr_t>(st)}];
-    if (!s) s = new WsSlot;
-    slot = s;
+  const WsKey key = ws_key(dev, st);
+  std::shared_ptr<WsSlot> slot;
+  std::unique_lock<std::mutex> lk;
+  for (;;) {
+    {
+      std::lock_guard<std::mutex> g(g_mu);
+      std::shared_ptr<WsSlot> &s = g_ws_slots[key];
+      if (!s) s = std::make_shared<WsSlot>();
+      slot = s;
+    }
+    lk = std::unique_lock<std::mutex>(slot->mu);
+    if (!slot->released) break;
+    lk.unlock();  // released between the lookup and the lock: take the slot that replaced it
   }
-  std::unique_lock<std::mutex> lk(slot->mu);
   if (slot->bytes < bytes) {
     size_t want = size_t(1) << 20;
     while (want < bytes) want <<= 1;
@@ -149,7 +169,32 @@ int library_workspace(size_t bytes, void *st, WorkspaceLease &lease) {
     slot->bytes = want;
   }
   lease.ptr = slot->ptr;
+  lease.keep = slot;
   lease.lock = std::move(lk);
+  return PK_OK;
+}
+
+int release_workspace(void *st) {
+  int dev = 0;
+  PK_HIP(hipGetDevice(&dev));
+  std::shared_ptr<WsSlot> slot;
+  {
+    std::lock_guard<std::mutex> g(g_mu);
+    auto it = g_ws_slots.find(ws_key(dev, st));
+    if (it == g_ws_slots.end()) return PK_OK;
+    slot = it->second;
+    g_ws_slots.erase(it);
+  }
+  // wait for a lease holder to finish enqueuing, then for the stream's
+  // queued kernels (the last readers of the buffers) before freeing them
+  std::lock_guard<std::mutex> lk(slot->mu);
+  slot->released = true;
+  PK_HIP(hipStreamSynchronize(static_cast<hipStream_t>(st)));
+  for (void *p : slot->retired) PK_HIP(hipFree(p));
+  slot->retired.clear();
+  if (slot->ptr) PK_HIP(hipFree(slot->ptr));
+  slot->ptr = nullptr;
+  slot->bytes = 0;
   return PK_OK;
 }
 
@@ -209,6 +254,13 @@ __global__ void probe_store_kernel(uint16_t *out) {
   if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = 0x3F80u;
 }
 
+// The launch-floor probe: no memory access; the dynamic LDS is reserved by
+// the launch (the never-taken store keeps the declaration live).
+__global__ void probe_empty_kernel(int never) {
+  extern __shared__ uint32_t probe_lds[];
+  if (never == 1) probe_lds[threadIdx.x] = 0u;
+}
+
 }  // namespace pk
 
 using namespace pk;
@@ -238,6 +290,18 @@ int pk_probe_invalid_launch(int *launch_status, int *sync_status) {
   return PK_OK;
 }
 
+// An empty kernel at a given grid, workgroup size and dynamic LDS: the
+// fixed cost of a launch of that geometry (dispatch, LDS allocation,
+// workgroup start and retirement), timed beside latency-bound kernels.
+int pk_probe_empty_launch(int blocks, int threads, int lds_bytes, void *stream) {
+  PK_CHECK_ARG(blocks > 0 && threads > 0 && threads <= 1024 && lds_bytes >= 0 && lds_bytes <= 160 * 1024,
+               "pk_probe_empty_launch: blocks %d, threads %d (1..1024), lds %d bytes (0..163840)", blocks,
+               threads, lds_bytes);
+  probe_empty_kernel<<<blocks, threads, (size_t)lds_bytes, (hipStream_t)stream>>>(0);
+  PK_LAUNCH_CHECK("pk_probe_empty_launch");
+  return PK_OK;
+}
+
 const char *pk_version(void) { return "polykernel_amd 0.1.0 gfx950"; }
 
 const char *pk_last_error(void) { return g_err; }
@@ -260,6 +324,8 @@ int pk_library_workspace(size_t bytes, void *stream, void **ptr) {
   if (rc == PK_OK) *ptr = lease.ptr;
   return rc;
 }
+
+int pk_release_workspace(void *stream) { return release_workspace(stream); }
 
 int pk_init(void) {
   const uint16_t *t = nullptr;

@@ -124,7 +124,10 @@ __global__ __launch_bounds__(kThreads) void naive_softmax_mask_kernel(const floa
   for (int c = 0; c < cols; ++c) y[base + c] = (uint16_t)f2bf(__fmul_rn(expf(__fsub_rn(z(c), m)), inv));
 }
 
-constexpr int kMaxD = 256;
+// Head dims up to the library's 1024; a thread keeps 256 output dims in
+// registers and takes the key loop again for each further 256 (every output
+// element still sums its keys in order).
+constexpr int kMaxD = 1024, kChunkD = 256;
 
 __global__ __launch_bounds__(64) void naive_attention_kernel(const uint16_t *__restrict__ Q,
                                                              const uint16_t *__restrict__ K,
@@ -146,16 +149,19 @@ __global__ __launch_bounds__(64) void naive_attention_kernel(const uint16_t *__r
   };
   float m = -INFINITY;
   for (int j = 0; j <= limit && j < S_kv; ++j) m = fmaxf(m, score(j));
-  float o[kMaxD];
-  for (int t = 0; t < D; ++t) o[t] = 0.0f;
-  float sum = 0.0f;
-  for (int j = 0; j <= limit && j < S_kv; ++j) {
-    const float w = expf(__fsub_rn(score(j), m));
-    sum = __fadd_rn(sum, w);
-    for (int t = 0; t < D; ++t) o[t] = __fadd_rn(o[t], __fmul_rn(w, bfv(vb[(int64_t)j * D + t])));
+  for (int c0 = 0; c0 < D; c0 += kChunkD) {
+    const int cn = min(kChunkD, D - c0);
+    float o[kChunkD];
+    for (int t = 0; t < cn; ++t) o[t] = 0.0f;
+    float sum = 0.0f;  // the same sum on every pass
+    for (int j = 0; j <= limit && j < S_kv; ++j) {
+      const float w = expf(__fsub_rn(score(j), m));
+      sum = __fadd_rn(sum, w);
+      for (int t = 0; t < cn; ++t) o[t] = __fadd_rn(o[t], __fmul_rn(w, bfv(vb[(int64_t)j * D + c0 + t])));
+    }
+    const float inv = __fdiv_rn(1.0f, sum);
+    for (int t = 0; t < cn; ++t) O[row * D + c0 + t] = (uint16_t)f2bf(__fmul_rn(o[t], inv));
   }
-  const float inv = __fdiv_rn(1.0f, sum);
-  for (int t = 0; t < D; ++t) O[row * D + t] = (uint16_t)f2bf(__fmul_rn(o[t], inv));
 }
 
 // ---- parity metrics -----------------------------------------------------------

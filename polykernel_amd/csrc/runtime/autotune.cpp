@@ -361,8 +361,8 @@ bool PrepareAttention(const Shape &s, const AutotuneOptions &o, DeviceArena &are
                       std::string &error) {
   const int Sq = (int)s.m, Skv = (int)s.n, D = (int)s.k, BH = std::max(1, o.batch_heads);
   const int Sc = Skv - Sq;
-  if (Sc < 0 || D <= 0 || D > 256) {
-    error = "fused_kv_append_attention: shape needs S_kv >= S_q and 0 < D <= 256";
+  if (Sc < 0 || D <= 0 || D > 1024) {
+    error = "fused_kv_append_attention: shape needs S_kv >= S_q and 0 < D <= 1024";
     return false;
   }
   const size_t q_n = (size_t)BH * Sq * D, kv_n = (size_t)BH * Skv * D;

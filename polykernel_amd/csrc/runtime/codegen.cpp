@@ -215,7 +215,7 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
     return true;
   }
   if (panel) {
-    if (c.block_k == e.shape.k && c.num_warps == 4) {  // whole-K panel kernel
+    if (runtime::IsPanelConfig(c, e.shape.k)) {  // whole-K panel kernel
       source = head + "#include \"gemm_kernels.hpp\"\n\n" +
                "extern \"C\" __global__ __launch_bounds__(256) void pk_panel(pk_panel_args a) {\n"
                "  pk::gk::rmsnorm_panel_fast_body(a);\n}\n";

@@ -17,6 +17,7 @@
 
 #include "../../../include/polykernel_amd_runtime.hpp"
 #include "../attention_module.hpp"
+#include "internal.hpp"
 #include "../gemm_args.h"
 #include "../int8_args.h"
 #include "../rowwise_args.h"
@@ -338,7 +339,7 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
     }
     if (!CheckEntry(e, p->M, p->N, p->K, error)) return false;
     const Config &c = e.best;
-    if (c.block_k == p->K && c.num_warps == 4) {
+    if (IsPanelConfig(c, p->K)) {
       if (!Aligned16(p->x) || !Aligned16(p->W) || (p->gamma && !Aligned16(p->gamma)) || !Aligned16(p->out)) {
         error = "code-object RMSNorm -> MatMul panel config {" + autotune::ToString(c) +
                 "} needs 16-byte aligned x, W, gamma and out";

@@ -55,8 +55,10 @@ ATT_SQ, ATT_SCACHE, ATT_HEAD_DIMS = 200, 256, (64, 128, 96, 256, 512, 300)
 # 131072 columns)
 ROW_ROWS, ROW_COLS = 37, (512, 1024, 2048, 4096, 8192, 16384, 32768, 65536, 70000, 131072, 140000, 1000, 999)
 # RMSNorm -> MatMul: the whole-K panel (ragged M) and the RMSNorm-into-
-# workspace path followed by a GEMM (K 1536 and 2048)
-PANEL_SHAPES = ((40, 136, 768), (64, 256, 1536), (72, 264, 2048))
+# workspace path followed by a GEMM (K 1536 and 2048); at K 64 the panel
+# (64 x 256), and the 64-deep GEMM configs whose block_k equals K: N % 8 != 0
+# (no panel) and more than 256 panel tiles (33 x 8)
+PANEL_SHAPES = ((40, 136, 768), (64, 256, 1536), (72, 264, 2048), (64, 256, 64), (40, 1001, 64), (1056, 512, 64))
 
 
 def conformance_entries() -> list:

@@ -128,6 +128,21 @@ def test_emit_source_rmsnorm_matmul_templates():
     assert "void pk_gemm(pk_gemm_args g)" in src
 
 
+def test_emit_source_rmsnorm_matmul_k64_gemm_configs_are_not_panels():
+    """At K = 64 the 64-deep GEMM configs (block_k 64, 4 waves) have
+    block_k == K like the panel config; only the 32 x 64 tile is the panel.
+    Every GEMM candidate must emit pk_gemm (the panel kernel needs N % 8 == 0
+    and one round of tiles), and the panel candidate pk_panel."""
+    for shape in ((4096, 1001, 64), (4096, 512, 64), (64, 256, 64)):
+        for cfg in rt.candidates("fused_rmsnorm_matmul", *shape):
+            src = rt.emit_source(gemm_entry("fused_rmsnorm_matmul", *shape, config=cfg))
+            panel = (cfg["block_m"], cfg["block_n"], cfg["block_k"]) == (32, 64, shape[2])
+            assert ("void pk_panel(" in src) == panel, (shape, cfg)
+            assert ("void pk_gemm(" in src) == (not panel), (shape, cfg)
+    # the small shape fits the panel, so its candidates include it
+    assert any((c["block_m"], c["block_n"]) == (32, 64) for c in rt.candidates("fused_rmsnorm_matmul", 64, 256, 64))
+
+
 @pytest.mark.skipif(shutil.which("hipcc") is None and not __import__("os").path.exists("/opt/rocm/bin/hipcc"),
                     reason="no hipcc")
 def test_emit_code_object_records_hash_and_invalidates(tmp_path):

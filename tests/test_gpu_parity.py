@@ -21,6 +21,7 @@ import pytest
 
 from polykernel_amd import metrics as mt
 from polykernel_amd import synth
+from tests.bounds import _abs_dot, _att_bound_bad, _err_bound_ok, _gate_bad, _gate_int8_bad, _int8_exact_inputs
 from tests.helpers import bf, f32, from_dev, int_bf16, rng_bf16, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -34,65 +35,6 @@ def K():
 
 def _say(msg):
     print(msg, flush=True)
-
-
-def _err_bound_ok(gpu_bits, ref_bits, abs_dot, Kdim, operand_ulps=0.0):
-    """Number of outputs outside |gpu - ref| <= 2 ulp_bf16(ref) + (K 2^-23 + u 2^-8) sum|a||b|.
-
-    K 2^-23 sum|a||b| bounds any fp32 summation order (two such sums differ by
-    at most twice the classic gamma_K bound); u 2^-8 sum|a||b| admits u bf16 ulps
-    of difference in each A operand (the fused RMSNorm prologue reduces the
-    row sum of squares in a different order, so a normalised activation can
-    round to the neighbouring bf16)."""
-    g, r = f32(gpu_bits).astype(np.float64), f32(ref_bits).astype(np.float64)
-    ulp = np.abs(r) * 2.0**-7 + 2.0**-133
-    bound = 2 * ulp + (Kdim * 2.0**-23 + operand_ulps * 2.0**-8) * abs_dot
-    bad = np.abs(g - r) > bound
-    return int(bad.sum())
-
-
-def _abs_dot(a_bits, b_bits):
-    return np.abs(f32(a_bits).astype(np.float64)) @ np.abs(f32(b_bits).astype(np.float64))
-
-
-def _gate_bad(epi, a, b, got, bias=None, r=None, operand_ulps=0.0):
-    """Outputs outside the device fp32 error model (pk_gate_matmul): got must be
-    the reference epilogue (bf16 GEMM epi 0 none, 1 bias+GELU, 2 bias+residual)
-    applied to some fp32 accumulation of a @ b's products.  Arguments are
-    device tensors (a row sample of A, R and got is enough: rows are
-    independent)."""
-    import ctypes
-
-    import torch
-
-    from polykernel_amd import _lib
-
-    n = ctypes.c_ulonglong(0)
-    M, Kd = a.shape
-    N = b.shape[1]
-    ptr = lambda t: None if t is None else t.data_ptr()
-    _lib.check(_lib.load().pk_gate_matmul(epi, ptr(a), ptr(b), ptr(bias), ptr(r), ptr(got), M, N, Kd,
-                                          float(operand_ulps), ctypes.byref(n),
-                                          torch.cuda.current_stream().cuda_stream), "pk_gate_matmul")
-    return n.value
-
-
-def _gate_int8_bad(epi, a, wq, s, got, r=None):
-    """As _gate_bad for the int8 weight-only GEMM (epi 0 none, 1 GELU, 2 residual)."""
-    import ctypes
-
-    import torch
-
-    from polykernel_amd import _lib
-
-    n = ctypes.c_ulonglong(0)
-    M, Kd = a.shape
-    N = wq.shape[1]
-    _lib.check(_lib.load().pk_gate_matmul_int8(epi, a.data_ptr(), wq.data_ptr(), s.data_ptr(),
-                                               None if r is None else r.data_ptr(), got.data_ptr(), M, N, Kd,
-                                               ctypes.byref(n), torch.cuda.current_stream().cuda_stream),
-               "pk_gate_matmul_int8")
-    return n.value
 
 
 # ------------------------------------------------------------------ elementwise / rows
@@ -210,6 +152,30 @@ def test_row_ops_every_config(gpu, oracle, rows, cols):
                 rep = mt.assert_correct(got, want_s, what=op)
                 assert rep.bit_exact >= 0.98, (cfg, rep)
                 assert np.all(f32(got)[mask == 0xFF80] == 0.0)
+
+
+@pytest.mark.parametrize("cols", [98304, 131072])
+def test_softmax_mask_rising_max_rows(gpu, oracle, cols):
+    """Rows of 65537-131072 columns take the packed-bf16 softmax, which sums
+    online: each lane's running sum is rescaled by exp(m_old - m_new) whenever
+    its running max grows, so the sum differs from the oracle's two-pass
+    sum of exp(z - m) in the last fp32 bits.  Rows whose max keeps rising (a
+    gentle and a steep ramp under noise: the max grows on nearly every chunk
+    a lane reads), one whose max falls and an ordinary one exercise that
+    rescaling against the row bars (>= 98 % bit-exact, <= 1 ulp)."""
+    rows = 4
+    c = np.arange(cols, dtype=np.float32)
+    logits = synth.normal_f32((rows, cols), 91, 1.0)
+    logits[0] += c * np.float32(30.0 / cols)
+    logits[1] += c * np.float32(200.0 / cols)
+    logits[2] -= c * np.float32(30.0 / cols)
+    mask = synth.mask_bf16((rows, cols), 92, 0.1)
+    _say(f"softmax rising max {cols}")
+    got = from_dev(K().fused_softmax_mask(to_dev(logits), to_dev(mask)))
+    want = oracle.softmax_mask(logits, mask)
+    rep = mt.assert_correct(got, want, what="softmax_mask rising max")
+    assert rep.bit_exact >= 0.98 and rep.max_ulp <= 1, rep
+    assert np.all(f32(got)[mask == 0xFF80] == 0.0)
 
 
 @pytest.mark.parametrize("cols", [1000, 8192, 65536, 131072])
@@ -449,18 +415,71 @@ def test_mlp_block_small(gpu, oracle):
     assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
 
 
+def _bf16_ulp(v):
+    """An upper bound on one bf16 ulp at magnitude |v| (and the subnormal step)."""
+    return np.abs(v) * 2.0**-7 + 2.0**-133
+
+
 def test_mlp_block_config2_row_sample(gpu, oracle):
     """Config 2 at full size on the GPU; rows are independent, so the oracle
-    checks a seeded sample of 16 rows."""
+    checks a seeded sample of 128 rows: the reference metrics on the block
+    output, and a per-element error model of the block output against the
+    oracle's whole chain.  With a = RMSNorm(x), t1 = bf16(bf16(a W1) + b1),
+    h = GELU(t1), t2 = bf16(bf16(h W2) + b2), y = bf16(t2 + x), and bf16
+    rounding monotone (|bf16(u) - bf16(v)| <= |u - v| + ulp):
+      |dh| <= 1.13 (sum_k |da_k| |W1_k| + 2 K1 2^-23 sum |a| |W1| + 2 ulp(acc1) + ulp(t1)) + ulp(h)
+      |dy| <= sum_k |dh_k| |W2_k| + 2 K2 2^-23 sum |h| |W2| + ulp(acc2) + ulp(t2) + ulp(y)
+    (1.13 bounds |GELU'| on the real line; da and dh are the measured
+    differences between the GPU's stages and the oracle's).  Any fp32
+    summation order meets it; a wrong index, sign or dropped term does not."""
+    import torch
+
     M, d, F = 4096, 4096, 16384
     _say("mlp_block config2 full")
     x, g, w1, b1, w2, b2 = _mlp_inputs(M, d, F)
-    got = from_dev(K().mlp_block(*map(to_dev, (x, g, w1, b1, w2, b2)), eps=1e-6))
-    rows = np.sort(np.random.default_rng(46).choice(M, 16, replace=False))
-    want = oracle.mlp_block(x[rows], g, w1, b1, w2, b2, 1e-6)
-    rep = mt.report(got[rows], want)
-    _say(f"mlp config2 sample: {rep}")
+    dx, dg, dw1, db1, dw2, db2 = map(to_dev, (x, g, w1, b1, w2, b2))
+    block = K().mlp_block(dx, dg, dw1, db1, dw2, db2, eps=1e-6)
+    rows = np.sort(np.random.default_rng(46).choice(M, 128, replace=False))
+    trows = torch.from_numpy(rows).cuda()
+    pick = lambda t: from_dev(t.index_select(0, trows).contiguous())
+    got = pick(block)
+    # the GPU's stages (the block is their chain, bit for bit)
+    da_ = K().rmsnorm(dx, dg, 1e-6)
+    dh_ = K().fused_matmul_bias_gelu(da_, dw1, db1)
+    dy_ = K().fused_matmul_bias_residual(dh_, dw2, db2, dx)
+    torch.cuda.synchronize()
+    assert torch.equal(block.view(torch.int16), dy_.view(torch.int16))
+    ga, gh = pick(da_), pick(dh_)
+    del da_, dh_, dy_, block
+    # the oracle's chain on the sample, which is its mlp_block
+    xs = x[rows]
+    oa = oracle.rmsnorm(xs, g, 1e-6)
+    oh = oracle.fused_matmul_bias_gelu(oa, w1, b1)
+    want = oracle.fused_matmul_bias_residual(oh, w2, b2, xs)
+    assert np.array_equal(want, oracle.mlp_block(xs, g, w1, b1, w2, b2, 1e-6))
+    rep = mt.report(got, want)
+    _say(f"mlp config2 sample (128 rows): {rep}")
     assert rep.cosine >= 0.999 and rep.pcc >= 0.99 and rep.bit_exact >= 0.9, rep
+    f = lambda b: f32(b).astype(np.float64)
+    w1f, w2f = f(w1), f(w2)
+    W1a, W2a = np.abs(w1f), np.abs(w2f)
+    acc1 = f(oa) @ w1f
+    dacc1 = np.abs(f(ga) - f(oa)) @ W1a + 2 * d * 2.0**-23 * (np.maximum(np.abs(f(ga)), np.abs(f(oa))) @ W1a)
+    t1 = f(oracle.bias(oracle.matmul(oa, w1), b1))
+    hmax = np.maximum(np.abs(f(gh)), np.abs(f(oh)))
+    # + 2^-18 |h|: the reference GELU's own fp32 rounding before its bf16 rounding
+    bh = 1.13 * (dacc1 + 2 * _bf16_ulp(np.abs(acc1) + dacc1) + _bf16_ulp(np.abs(t1) + dacc1 + _bf16_ulp(acc1))) \
+        + _bf16_ulp(hmax) + 2.0**-18 * hmax
+    dh = np.abs(f(gh) - f(oh))
+    assert int((dh > bh).sum()) == 0, "h outside its error model"
+    del acc1, dacc1, t1, bh, w1f, W1a
+    acc2 = f(oh) @ w2f
+    dacc2 = dh @ W2a + 2 * F * 2.0**-23 * (hmax @ W2a)
+    t2 = acc2 + f(b2)
+    by = dacc2 + 2 * _bf16_ulp(np.abs(acc2) + dacc2) + _bf16_ulp(np.abs(t2) + 2 * dacc2) \
+        + _bf16_ulp(np.abs(t2 + f(xs)) + 3 * dacc2)
+    bad = int((np.abs(f(got) - f(want)) > by).sum())
+    assert bad == 0, (bad, rep)
 
 
 def test_mlp_block_config2_stages_error_model(gpu, oracle):
@@ -521,17 +540,6 @@ _I8S_VARIANTS = [(16, 512, 4, 3), (16, 448, 4, 3), (16, 256, 2, 6), (16, 256, 4,
                  (16, 512, 2, 4), (16, 128, 4, 6), (16, 64, 4, 6), (16, 448, 4, 4),
                  (32, 512, 4, 3), (32, 256, 4, 4), (32, 128, 4, 6),
                  (64, 512, 4, 2), (64, 256, 4, 3), (64, 128, 4, 3)]
-
-
-def _int8_exact_inputs(M, N, Kd, seed):
-    """Integer-valued activations, int8 weights, power-of-two scales: every
-    partial sum is an integer below 2^24, so any summation order is exact and
-    the GPU must match the oracle bit for bit."""
-    a = int_bf16((M, Kd), seed, -4, 4)
-    r = np.random.default_rng(seed + 1)
-    wq = r.integers(-127, 128, size=(Kd, N)).astype(np.int8)
-    s = (2.0 ** r.integers(-9, -4, size=N)).astype(np.float32)
-    return a, wq, s
 
 
 @pytest.mark.parametrize("bm,bn,waves,stages", _I8S_VARIANTS)
@@ -613,27 +621,6 @@ def test_decode_mlp_int8_config5(gpu, oracle):
 
 
 # ------------------------------------------------------------------ attention
-
-def _att_bound_bad(oracle, got, want, q, k, v, causal):
-    """Outputs outside an fp32 error model of softmax attention.
-
-    A weight w_j = exp(s_j - m) carries a relative error eps_w <= D 2^-23 scale
-    max_j sum_d |q_d k_jd| (score summation order) + 2^-20 (exp) + 2^-16 (the
-    bf16 hi/lo split of p); the output o = sum w v / sum w then moves by at most
-    2 eps_w (sum w |v| / sum w + |o|), plus S_kv 2^-23 sum w |v| / sum w for the
-    PV summation order, plus 2 bf16 ulp of the final rounding."""
-    D, Skv = q.shape[-1], k.shape[2]
-    scale = 1.0 / np.sqrt(D)
-    qa = np.abs(f32(q).astype(np.float64))
-    ka = np.abs(f32(k).astype(np.float64))
-    max_qk = float(np.max(qa @ np.swapaxes(ka, -1, -2)))
-    eps_w = D * 2.0**-23 * scale * max_qk + 2.0**-20 + 2.0**-16
-    abs_att = f32(oracle.attention_prefill(q, k, v & 0x7FFF, None, causal)).astype(np.float64) * 1.01
-    r = f32(want).astype(np.float64)
-    g = f32(got).astype(np.float64)
-    bound = 2 * (np.abs(r) * 2.0**-7 + 2.0**-133) + (2 * eps_w + Skv * 2.0**-23) * (abs_att + np.abs(r))
-    return int((np.abs(g - r) > bound).sum())
-
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 2, 32, 32, 32), (2, 4, 16, 16, 64), (1, 1, 24, 24, 40),
@@ -805,7 +792,7 @@ def test_attention_leaky_mask_is_detected(gpu, oracle):
 
 def test_fused_kv_append_attention_config3_heads(gpu, oracle):
     """Config 3 geometry (H=32, D=128, 3584 cached + 512 new, in-place append);
-    the oracle checks 2 of the 32 heads plus the appended cache bit-exactly."""
+    the oracle checks all 32 heads plus the appended cache bit-exactly."""
     import torch
 
     B, H, Sc, Sn, D = 1, 32, 3584, 512, 128
@@ -821,7 +808,7 @@ def test_fused_kv_append_attention_config3_heads(gpu, oracle):
     got = from_dev(K().fused_kv_append_attention(to_dev(q), to_dev(kn), to_dev(vn), kcd, vcd, Sc))
     kfull, vfull = oracle.kv_append(kc, kn), oracle.kv_append(vc, vn)
     assert np.array_equal(from_dev(kcd), kfull) and np.array_equal(from_dev(vcd), vfull)
-    heads = [0, 17]
+    heads = list(range(H))
     want = oracle.attention_prefill(q[:, heads], kfull[:, heads], vfull[:, heads], None, True)
     rep = mt.report(got[:, heads], want)
     _say(f"attention config3 heads {heads}: {rep}")

@@ -139,3 +139,54 @@ def test_dma_gemm_a_operand_beyond_4gib(gpu, oracle):
     assert bad.size == 0, f"rows {rows[bad][:10]} differ"
     del A, C
     torch.cuda.empty_cache()
+
+
+def test_release_workspace_and_per_thread_stream(gpu):
+    """pk_release_workspace frees a stream's library workspace once the
+    stream's queued kernels are done: a split-K int8 launch on a new stream,
+    the release, the stream dropped, three times over (a new stream may reuse
+    the handle), every output equal to the default stream's; releasing a
+    stream without a slot is a no-op.  hipStreamPerThread gives each host
+    thread its own buffer, and each thread releases its own."""
+    import ctypes
+
+    import torch
+
+    from polykernel_amd import _lib, kernels
+    from polykernel_amd import runtime as rt
+
+    lib = _lib.load()
+    assert rt.default_config("matmul_int8", 16, 4096, 8192)["block_k"] < 8192
+    a, wq, s = _int8_case(7)
+    want = from_dev(kernels.matmul_int8(a, wq, s))
+    for rnd in range(3):
+        _say(f"release round {rnd}")
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            out = kernels.matmul_int8(a, wq, s)
+        _lib.check(lib.pk_release_workspace(st.cuda_stream), "pk_release_workspace")
+        assert np.array_equal(from_dev(out), want)
+        _lib.check(lib.pk_release_workspace(st.cuda_stream), "pk_release_workspace (no slot)")
+        del st, out
+
+    per_thread = 2  # hipStreamPerThread
+    ptrs, errors = {}, []
+    both = threading.Barrier(2)
+
+    def grab(i):
+        try:
+            p = ctypes.c_void_p()
+            _lib.check(lib.pk_library_workspace(1 << 20, per_thread, ctypes.byref(p)), "pk_library_workspace")
+            ptrs[i] = p.value
+            both.wait(timeout=60)  # both threads alive: distinct thread ids
+            _lib.check(lib.pk_release_workspace(per_thread), "pk_release_workspace")
+        except Exception as e:  # noqa: BLE001 -- re-raised in the main thread
+            errors.append(e)
+
+    ts = [threading.Thread(target=grab, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert ptrs[0] and ptrs[1] and ptrs[0] != ptrs[1], ptrs

@@ -131,3 +131,36 @@ def test_grid_limits_are_refused_before_launch():
     res = subprocess.run([sys.executable, "-c", _GRID_CHILD, str(ROOT)], capture_output=True, text=True, timeout=300)
     assert res.returncode == 0 and res.stdout.strip().endswith("ok"), \
         f"child exited {res.returncode}:\n{res.stdout[-2000:]}\n{res.stderr[-2000:]}"
+
+
+_REFUSAL_CHILD = r"""
+import ctypes as C, sys
+sys.path.insert(0, sys.argv[1])
+from polykernel_amd import _lib
+from polykernel_amd import runtime as rt
+lib = _lib.load()
+# launch_matmul_int8_noalloc: split-K partials beyond its 16 MiB static
+# buffer are refused before any device call (plausible non-null pointers,
+# never dereferenced)
+M, N, Kd = 128, 28672, 8192
+cfg = rt.default_config("matmul_int8", M, N, Kd)
+splits = -(-Kd // cfg["block_k"])
+assert splits > 1 and splits * M * N * 4 > (16 << 20), (cfg, splits)
+rc = lib.launch_matmul_int8_noalloc(16, 16, 16, 16, M, N, Kd, None)
+assert rc == _lib.PK_ERR_WORKSPACE and "static buffer" in _lib.last_error(), (rc, _lib.last_error())
+# pk_probe_empty_launch: a geometry outside the device limits is refused
+for blocks, threads, lds in ((0, 256, 0), (1, 0, 0), (1, 1025, 0), (1, 64, -1), (1, 64, 160 * 1024 + 4)):
+    rc = lib.pk_probe_empty_launch(blocks, threads, lds, None)
+    assert rc == _lib.PK_ERR_INVALID_ARG and "pk_probe_empty_launch" in _lib.last_error(), (blocks, threads, lds)
+print("ok")
+"""
+
+
+def test_refusals_before_any_device_call():
+    """Argument checks that must fail before the library touches a device:
+    launch_matmul_int8_noalloc's scratch limit and the launch-floor probe's
+    geometry limits (run in a child process, no GPU needed)."""
+    res = subprocess.run([sys.executable, "-c", _REFUSAL_CHILD, str(ROOT)], capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), \
+        f"child exited {res.returncode}:\n{res.stdout[-2000:]}\n{res.stderr[-2000:]}"
