@@ -1,13 +1,19 @@
 """Correctness-gated autotuner CLI: sweep the gfx950 variants of an op on the
 current GPU and write the winners into a tuning-cache file.
 
-    python -m polykernel_amd.autotune --baseline --out polykernel_amd/tuning/gfx950.json
+    python -m polykernel_amd.autotune --baseline --out polykernel_amd/tuning/gfx950.json \
+        --log polykernel_amd/tuning/gfx950.sweep.jsonl
     python -m polykernel_amd.autotune --op matmul_int8 --shape 16,28672,8192
 
 Each (op, shape) goes through pk_autotune (csrc/runtime/autotune.cpp): every
 candidate is compared with a naive device golden and gated (cosine >= 0.999,
 pcc >= 0.99, max_rel_err <= the reference's ceiling rule) before it is timed;
-the fastest validated variant becomes the entry.  Entries are merged into
+the fastest validated variant becomes the entry.  GEMM-class ops are also
+gated on the per-element fp32 error model (model_violations must be 0).
+--log writes one JSON line per swept variant (config, its metrics, model
+violations, validated, median time) -- the record of what each committed
+entry passed, since the entry itself keeps only the schema's fields.
+Entries are merged into
 the output file (last writer wins per (gpu, op, shape)), which is the
 tuning-cache document of tuning/schema.json and loads with
 runtime.KernelCache.load_tuning_cache -- the default cache of
@@ -63,6 +69,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rounds", type=int, default=5, help="interleaved timing passes over the gated variants")
     ap.add_argument("--max-variants", type=int, default=None)
+    ap.add_argument("--log", type=Path, help="write every swept variant's gate outcome here (JSON lines)")
     ap.add_argument("--verbose", action="store_true")
     args = ap.parse_args(argv)
     if args.baseline == bool(args.op):
@@ -71,7 +78,7 @@ def main(argv=None) -> int:
     opts = dict(iters=args.iters, warmup=args.warmup, rounds=args.rounds, verbose=args.verbose)
     if args.max_variants:
         opts["max_variants"] = args.max_variants
-    entries, failed = [], 0
+    entries, failed, log = [], 0, []
     for op, m, n, k in jobs:
         t0 = time.time()
         res = rt.autotune(op, m, n, k, **opts)
@@ -82,9 +89,15 @@ def main(argv=None) -> int:
               flush=True)
         failed += not e["validated"]
         entries.append(e)
+        for v in res["variants"]:
+            log.append({"op": op, "shape": [m, n, k], "selected": v["config"] == e["best"], **v})
     if args.out:
         merge(args.out, entries)
         print(f"[autotune] wrote {len(entries)} entries to {args.out}", flush=True)
+    if args.log:
+        args.log.parent.mkdir(parents=True, exist_ok=True)
+        args.log.write_text("".join(json.dumps(r, sort_keys=True) + "\n" for r in log))
+        print(f"[autotune] wrote {len(log)} variant records to {args.log}", flush=True)
     return 1 if failed else 0
 
 
