@@ -221,6 +221,36 @@ class Timer:
         return sorted(means)[1]
 
 
+def graph_time(launch, n: int = 100, reps: int = 20) -> float:
+    """ms per launch of launch(stream) captured n times in a HIP graph on a side
+    stream and replayed `reps` times (median): the GPU time of back-to-back
+    launches without the host's per-launch cost.  launch must not allocate or
+    set memory (nothing to capture but kernels)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert launch(s.cuda_stream) == 0
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            sp = torch.cuda.current_stream().cuda_stream
+            for _ in range(n):
+                assert launch(sp) == 0
+    for _ in range(5):
+        gr.replay()
+    torch.cuda.synchronize()
+    t = []
+    for _ in range(reps):
+        e0, e1 = event_pair()
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        t.append(e0.elapsed_time(e1) / n)
+    return sorted(t)[reps // 2]
+
+
 def host_info() -> dict:
     """The host the CPU baselines ran on: usable cores and CPU model."""
     model = "unknown"
@@ -322,10 +352,17 @@ def bench_cfg1(t: Timer, cpu: bool) -> dict:
     big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
     ms_cold = t(run, key="cold", flush=lambda: big.fill_(1))
     # the fixed cost of a launch of the panel kernel's geometry (192 workgroups
-    # of 256 threads, 144 KiB of dynamic LDS), timed the same way
+    # of 256 threads, 144 KiB of dynamic LDS): launched from this loop the empty
+    # kernel is bound by the host's launch rate, so its GPU-side cost comes from
+    # a replayed HIP graph of 100 launches, and config 1 is timed that way too
     tiles, lds = (128 // 32) * (3072 // 64), 768 * 128 + 32 * 768 * 2
     floor = lambda: check(lib.pk_probe_empty_launch(tiles, 256, lds, t.sp), "empty launch")
-    ms_floor = t(floor, key="floor")
+    ms_floor_eager = t(floor, key="floor")
+    want = o.clone()
+    ms_graph = graph_time(lambda sp: lib.launch_fused_rmsnorm_matmul_gamma(
+        x.data_ptr(), g.data_ptr(), w.data_ptr(), o.data_ptr(), 128, 3072, 768, 1e-6, sp))
+    graph_equal = bool(torch.equal(o.view(torch.int16), want.view(torch.int16)))
+    ms_floor = graph_time(lambda sp: lib.pk_probe_empty_launch(tiles, 256, lds, sp))
     flop = 2 * 128 * 3072 * 768
     roof_us = CFG1_BYTES / (PEAK_HBM_GBS * 1e9) * 1e6
 
@@ -337,10 +374,14 @@ def bench_cfg1(t: Timer, cpu: bool) -> dict:
            "warm": t.stats["warm"], "cold_us": round(ms_cold * 1e3, 2), "cold": t.stats["cold"],
            "roofline": {"bound": "hbm", "unit": "GB/s", "peak": PEAK_HBM_GBS, "bytes": CFG1_BYTES,
                         "time_at_peak_us": round(roof_us, 3), "warm": roof(ms), "cold": roof(ms_cold),
+                        "graph": roof(ms_graph),
                         "mfma_time_at_peak_us": round(flop / (PEAK_BF16_TFLOPS * 1e12) * 1e6, 3)},
-           "launch_floor_us": round(ms_floor * 1e3, 2), "launch_floor": t.stats["floor"],
-           "note": "warm: L2/MALL-resident (5.7 MB); cold: a 1 GiB buffer written between launches; "
-                   "launch_floor: an empty kernel with the panel kernel's grid, workgroup and LDS"}
+           "graph_us": round(ms_graph * 1e3, 2), "graph_output_equal": graph_equal,
+           "launch_floor_us": round(ms_floor * 1e3, 2), "launch_floor_eager_us": round(ms_floor_eager * 1e3, 2),
+           "note": "warm: L2/MALL-resident (5.7 MB), launched back to back; cold: a 1 GiB buffer written between "
+                   "launches; graph_us: per launch in a replayed HIP graph of 100 launches (GPU time, no host "
+                   "launch cost); launch_floor_us: an empty kernel with the panel kernel's grid, workgroup and "
+                   "LDS in such a graph (launch_floor_eager_us: the same launched from the loop, host-bound)"}
     del big
     if cpu:
         from oracle import pyoracle

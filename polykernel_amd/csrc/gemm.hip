@@ -286,7 +286,7 @@ int fused_rmsnorm_matmul(const uint16_t *x, const uint16_t *gamma, const uint16_
                         aligned16(W) && (!gamma || aligned16(gamma));
   if (panel_ok && fast_panel_fits(M, N, K) && aligned16(out)) {
     const int tiles = ((M + RQ_BM - 1) / RQ_BM) * ((N + RQ_BN - 1) / RQ_BN);
-    const size_t lds = (size_t)K * 128 + (size_t)RQ_BM * K * 2;
+    const size_t lds = pk_panel_lds_bytes(K);
     rmsnorm_panel_gemm_fast_kernel<<<tiles, RQ_THREADS, lds, st>>>(
         PanelArgs{x, gamma, W, out, M, N, K, 1.0f / (float)K, eps});
     PK_LAUNCH_CHECK(name);

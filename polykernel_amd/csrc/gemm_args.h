@@ -27,4 +27,15 @@ typedef struct pk_panel_args {
   float inv_cols, eps;    /* 1 / K and the RMSNorm epsilon */
 } pk_panel_args;
 
+/* Launch geometry of the whole-K panel kernel (rmsnorm_panel_fast_body), for
+ * every host that launches it: 8 waves per 32 x 64 output tile, and dynamic
+ * LDS for the W slice (K x 64 bf16) and the normalised x panel (32 x K bf16),
+ * at least the three fp32 32 x 64 partial tiles its K parts are summed
+ * through at the end. */
+#define PK_PANEL_THREADS 512
+static inline unsigned pk_panel_lds_bytes(int K) {
+  const unsigned need = (unsigned)K * 128u + 64u * (unsigned)K;
+  return need > 24576u ? need : 24576u;
+}
+
 #endif /* PK_GEMM_ARGS_H */

@@ -715,20 +715,27 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
 
 // Latency-oriented RMSNorm -> MatMul for short rows (K <= 832, the config-1
 // fragment: a few MB, cache-resident, so one memory round trip dominates).
-// A workgroup of 4 waves owns 32 rows x 64 columns:
+// A workgroup of 8 waves owns 32 rows x 64 columns:
 //   - load the 32 x K panel of x (and gamma) into registers, then issue the
 //     whole 64-column slice of W (K x 64, 128 K bytes) as buffer_load ... lds
 //     DMA into LDS, every load in flight at once (loads complete in order, so
 //     x first lets the normalisation start while W still arrives: 8.50 ->
 //     8.34 us per config-1 launch);
-//   - 8 lanes per row reduce the sum of squares (shuffles), normalise
+//   - 16 lanes per row reduce the sum of squares (shuffles), normalise
 //     x / rms * gamma exactly as the reference and store the bf16 panel in LDS
 //     while W is still arriving;
-//   - wave w computes column block w & 1 over K half w >> 1 (MFMA 32x32x16),
-//     the halves are added in LDS and the tile is stored 16 bytes at a time.
-constexpr int RQ_BM = 32, RQ_BN = 64, RQ_THREADS = 256;
+//   - wave w computes column block w & 1 over K quarter w >> 1 (MFMA
+//     32x32x16), the quarters are added in LDS in order and the tile is
+//     stored 16 bytes at a time.
+// With one wave per SIMD (4 waves, K halves) each wave normalised 96 elements
+// of x and ran a 24-deep chain of dependent MFMAs; 8 waves halve both:
+// config 1 7.83 -> 6.67 us per launch in a replayed graph (every output within
+// the same error model; 99.07 % bit-exact to the oracle either way).
+constexpr int RQ_BM = 32, RQ_BN = 64, RQ_THREADS = PK_PANEL_THREADS;
 constexpr int RQ_MAX_K = 832;  // panel 64 K bytes + W slice 128 K bytes <= 160 KiB
-constexpr int RQ_XPT = RQ_MAX_K / 64;  // x chunks (16 B) per thread at most
+constexpr int RQ_TPR = RQ_THREADS / RQ_BM;         // threads per x row (16)
+constexpr int RQ_XPT = (RQ_MAX_K / 8 + RQ_TPR - 1) / RQ_TPR;  // x chunks (16 B) per thread at most
+constexpr int RQ_KP = RQ_THREADS / 64 / 2;         // K parts (waves per column block)
 
 __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
 #pragma clang fp contract(off)
@@ -749,17 +756,17 @@ __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
   const int m0 = mt * RQ_BM, n0 = nt * RQ_BN;
   const int kchunks = K >> 3;
 
-  // ---- x panel -> registers: thread t owns row t / 8, chunks (t % 8) + 8 j
-  const int r = tid >> 3, c0 = tid & 7;
+  // ---- x panel -> registers: thread t owns row t / 16, chunks (t % 16) + 16 j
+  const int r = tid / RQ_TPR, c0 = tid % RQ_TPR;
   const int gm = m0 + r;
-  const int nxc = (kchunks - c0 + 7) / 8;  // chunks of this thread
+  const int nxc = (kchunks - c0 + RQ_TPR - 1) / RQ_TPR;
   u32x4 xv[RQ_XPT], gv[RQ_XPT];
 #pragma unroll
   for (int j = 0; j < RQ_XPT; ++j) {
     xv[j] = u32x4{0, 0, 0, 0};
     gv[j] = u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 (no gamma)
     if (j < nxc) {
-      const int c = c0 + 8 * j;
+      const int c = c0 + RQ_TPR * j;
       if (gm < M) xv[j] = *reinterpret_cast<const u32x4 *>(X + (size_t)gm * K + c * 8);
       if (gamma) gv[j] = *reinterpret_cast<const u32x4 *>(gamma + c * 8);
     }
@@ -786,9 +793,8 @@ __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
       ss += a * a;
       ss += b * b;
     }
-  ss += __shfl_xor(ss, 1, 64);
-  ss += __shfl_xor(ss, 2, 64);
-  ss += __shfl_xor(ss, 4, 64);
+#pragma unroll
+  for (int o = 1; o < RQ_TPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
   const float rms = sqrtf(ss * inv_cols + eps);
   // x / rms: the three-operation exact division (div_fast) when every
   // numerator and divisor of the wave is in its range, else the IEEE division
@@ -807,7 +813,7 @@ __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
 #pragma unroll
     for (int j = 0; j < RQ_XPT; ++j) {
       if (j < nxc) {
-        const int c = c0 + 8 * j;
+        const int c = c0 + RQ_TPR * j;
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -834,9 +840,9 @@ __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
   vm_wait<0>();     // this wave's W loads have landed
   __syncthreads();  // everyone's W loads and panel stores
 
-  // ---- MFMA: wave -> (column block wid & 1, K half wid >> 1)
-  const int cb = wid & 1, kh = wid >> 1;
-  const int ks = K / 32;  // 16-k steps per half
+  // ---- MFMA: wave -> (column block wid & 1, K part wid >> 1 of RQ_KP)
+  const int cb = wid & 1, kp = wid >> 1;
+  const int ks = K / (16 * RQ_KP);  // 16-k steps per part
   const int grp = lane >> 4, gi = lane & 15;
   const int b_krow = 8 * (grp >> 1) + (gi >> 2);
   const int b_col = cb * 32 + 16 * (grp & 1) + 4 * (gi & 3);
@@ -844,7 +850,7 @@ __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
   f32x16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-  for (int s = kh * ks; s < (kh + 1) * ks; ++s) {
+  for (int s = kp * ks; s < (kp + 1) * ks; ++s) {
     const int c = 2 * s + (lane >> 5);
     const bf16x8 af = lds_read_a(Ap + a_row * K + ((c ^ (a_row & 7)) << 3));
     i16x4 hb[2];
@@ -858,25 +864,28 @@ __device__ __forceinline__ void rmsnorm_panel_fast_body(const PanelArgs &a) {
         af, __builtin_bit_cast(bf16x8, __builtin_shufflevector(hb[0], hb[1], 0, 1, 2, 3, 4, 5, 6, 7)), acc, 0, 0,
         0);
   }
-  // ---- add the K halves (fixed order: half 0 + half 1) and store
-  __syncthreads();  // everyone is done reading W: reuse its region (>= 8 KiB)
-  float *red = reinterpret_cast<float *>(Bs);  // [32][64] fp32
-  if (kh == 1) {
+  // ---- add the K parts in order (part 0 + part 1 + ...) and store
+  __syncthreads();  // everyone is done reading W: reuse its region (pk_panel_lds_bytes keeps >= 24 KiB)
+  float *red = reinterpret_cast<float *>(Bs);  // [RQ_KP - 1][32][64] fp32
+  if (kp > 0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-      red[((i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)) * RQ_BN + cb * 32 + (lane & 31)] = acc[i];
+      red[(kp - 1) * RQ_BM * RQ_BN + ((i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)) * RQ_BN + cb * 32 + (lane & 31)] = acc[i];
   }
   __syncthreads();
-  if (kh == 0) {
+  if (kp == 0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float *p = red + ((i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)) * RQ_BN + cb * 32 + (lane & 31);
-      *p = acc[i] + *p;
+      const int o = ((i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)) * RQ_BN + cb * 32 + (lane & 31);
+      float v = acc[i];
+#pragma unroll
+      for (int q = 1; q < RQ_KP; ++q) v = v + red[(q - 1) * RQ_BM * RQ_BN + o];
+      red[o] = v;
     }
   }
   __syncthreads();
-  {
-    const int rr = tid >> 3, c8 = (tid & 7) * 8;  // 32 rows x 8 chunks of 8 columns
+  if (tid < RQ_BM * 8) {
+    const int rr = tid >> 3, c8 = (tid & 7) * 8;
     const int m = m0 + rr, n = n0 + c8;
     if (m < M && n < N) {
       const float *p = red + rr * RQ_BN + c8;

@@ -217,7 +217,8 @@ bool EmitSource(const CacheEntry &e, std::string &source, std::string &error) {
   if (panel) {
     if (runtime::IsPanelConfig(c, e.shape.k)) {  // whole-K panel kernel
       source = head + "#include \"gemm_kernels.hpp\"\n\n" +
-               "extern \"C\" __global__ __launch_bounds__(256) void pk_panel(pk_panel_args a) {\n"
+               "extern \"C\" __global__ __launch_bounds__(" + std::to_string(PK_PANEL_THREADS) +
+               ") void pk_panel(pk_panel_args a) {\n"
                "  pk::gk::rmsnorm_panel_fast_body(a);\n}\n";
       return true;
     }

@@ -68,7 +68,7 @@ long long ConfigSpace::LdsBytes(std::string_view op, const Shape &shape, const C
     }
     case Family::RmsnormMatmul:
       // whole-K kernel: W slice (K x 64) + normalised panel (32 x K)
-      if (runtime::IsPanelConfig(c, shape.k)) return shape.k * 128LL + (long long)c.block_m * shape.k * 2;
+      if (runtime::IsPanelConfig(c, shape.k)) return pk_panel_lds_bytes((int)shape.k);
       return 2LL * c.shared_memory_stages * ((long long)c.block_m * c.block_k + (long long)c.block_k * c.block_n);
     case Family::Attention:
       // K/V ring + the query-group merge buffer it aliases

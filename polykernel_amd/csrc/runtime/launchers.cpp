@@ -352,8 +352,8 @@ LaunchFn CodeObjectPanelLauncher(std::shared_ptr<ModuleTable> table) {
       pk_panel_args a{p->x, p->gamma, p->W, p->out, p->M, p->N, p->K, 1.0f / (float)p->K, p->eps};
       unsigned tiles = 0;
       if (!TileGrid(p->M, p->N, p->K, 32, 64, tiles, error)) return false;
-      const unsigned lds = (unsigned)(p->K * 128 + 32 * p->K * 2);
-      return ModuleLaunch(mod->fns[0], tiles, 1, 256u, p->stream, a, "pk_panel", error, lds);
+      return ModuleLaunch(mod->fns[0], tiles, 1, (unsigned)PK_PANEL_THREADS, p->stream, a, "pk_panel", error,
+                          pk_panel_lds_bytes(p->K));
     }
     // GEMM config: the row normalisation, then the plain GEMM
     const bool dma = c.block_k == 32;

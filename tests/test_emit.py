@@ -117,7 +117,7 @@ def test_emit_source_rmsnorm_matmul_templates():
     and, otherwise, RMSNorm at the (M, K) row config followed by the config's
     GEMM."""
     src = rt.emit_source(gemm_entry("fused_rmsnorm_matmul", 128, 3072, 768))
-    assert "__launch_bounds__(256) void pk_panel(pk_panel_args a) {\n  pk::gk::rmsnorm_panel_fast_body(a);" in src
+    assert "__launch_bounds__(512) void pk_panel(pk_panel_args a) {\n  pk::gk::rmsnorm_panel_fast_body(a);" in src
     # past one round of panel tiles (M 300, N 4096): RMSNorm into workspace and the GEMM
     assert "pk_panel" not in rt.emit_source(gemm_entry("fused_rmsnorm_matmul", 300, 4096, 768))
     e = gemm_entry("fused_rmsnorm_matmul", 72, 264, 2048)
@@ -130,7 +130,7 @@ def test_emit_source_rmsnorm_matmul_templates():
 
 def test_emit_source_rmsnorm_matmul_k64_gemm_configs_are_not_panels():
     """At K = 64 the 64-deep GEMM configs (block_k 64, 4 waves) have
-    block_k == K like the panel config; only the 32 x 64 tile is the panel.
+    block_k == K like the panel config; only the 32 x 64 tile (8 waves) is the panel.
     Every GEMM candidate must emit pk_gemm (the panel kernel needs N % 8 == 0
     and one round of tiles), and the panel candidate pk_panel."""
     for shape in ((4096, 1001, 64), (4096, 512, 64), (64, 256, 64)):
