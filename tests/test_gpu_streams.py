@@ -190,3 +190,47 @@ def test_release_workspace_and_per_thread_stream(gpu):
         t.join(timeout=120)
     assert not errors, errors
     assert ptrs[0] and ptrs[1] and ptrs[0] != ptrs[1], ptrs
+
+
+def test_rmsnorm_matmul_panel_in_a_replayed_graph(gpu):
+    """The config-1 RMSNorm -> MatMul launch (the whole-K panel kernel, which
+    allocates nothing) captured into a HIP graph gives the eager bits on every
+    replay, with eager launches and synchronisations between the replays (the
+    bench times config 1 and its launch floor this way)."""
+    import ctypes
+
+    import torch
+
+    from polykernel_amd import _lib, synth
+
+    lib = _lib.load()
+    x = to_dev(synth.normal_bf16((128, 768), 11))
+    g = to_dev(synth.normal_bf16((768,), 12, 0.1, 1.0))
+    w = to_dev(synth.normal_bf16((768, 3072), 13, 1 / np.sqrt(768)))
+    o = torch.empty(128, 3072, dtype=torch.bfloat16, device="cuda")
+    eager = torch.empty_like(o)
+
+    def launch(out, sp):
+        return lib.launch_fused_rmsnorm_matmul_gamma(x.data_ptr(), g.data_ptr(), w.data_ptr(), out.data_ptr(),
+                                                     128, 3072, 768, ctypes.c_float(1e-6), sp)
+
+    assert launch(eager, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert launch(o, s.cuda_stream) == 0
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            sp = torch.cuda.current_stream().cuda_stream
+            for _ in range(4):
+                assert launch(o, sp) == 0
+    for rep in range(5):
+        o.fill_(0)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        _say(f"graph replay {rep}")
+        assert torch.equal(o.view(torch.int16), eager.view(torch.int16)), rep
+        assert launch(eager, torch.cuda.current_stream().cuda_stream) == 0  # eager work between replays
+        torch.cuda.synchronize()
