@@ -99,7 +99,8 @@ __global__ void bf16_selfcheck_kernel(unsigned long long *bad) {
 // Self-check of the paired GELU: for every low code (all 65536) and four
 // high-code patterns, gelu_pair_common (where gelu_pair_special finds neither
 // code outside its domain) and the dispatch the GEMM epilogue uses must equal
-// gelu_bits of each code.
+// gelu_bits of each code, and the epilogue's accumulated vote (GeluVote) must
+// flag exactly the pairs gelu_pair_special flags.
 __global__ void gelu_pair_selfcheck_kernel(const uint16_t *tab, unsigned long long *bad) {
   const uint32_t lo = blockIdx.x * blockDim.x + threadIdx.x;
   if (lo >= 65536u) return;
@@ -111,6 +112,10 @@ __global__ void gelu_pair_selfcheck_kernel(const uint16_t *tab, unsigned long lo
     if (!gelu_pair_special(w)) n += gelu_pair_common(w, tab) != want;
     const uint32_t got = gelu_pair_special(w) ? gelu_pair_exact(w, tab) : gelu_pair_common(w, tab);
     n += got != want;
+    // the accumulated vote of the GEMM epilogue agrees with gelu_pair_special
+    GeluVote v = gelu_vote_init();
+    gelu_vote_add(v, w & 0x7FFF7FFFu);
+    n += gelu_vote_special(v) != (gelu_pair_special(w) != 0u);
   }
   if (n) atomicAdd(bad, n);
 }

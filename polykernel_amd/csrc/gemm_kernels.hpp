@@ -457,9 +457,20 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
+  // With the GELU epilogue the product is formed transposed (W fragment as the
+  // MFMA's first operand): acc[fm][fn] then holds the 32 x 32 block with lane l
+  // owning output row fm*32 + l%32 and, per q, the 4 consecutive columns
+  // fn*32 + 8q + 4*(l/32) + (0..3), so the epilogue works on row-contiguous
+  // registers without staging the tile through LDS.  Each output is the same
+  // exact bf16 products summed in the same k order.
+  constexpr bool TRANSPOSED = EPI == EPI_BIAS_GELU;
   auto mfma_one = [&](const Frag &f, int i) {
-    acc[i / FN][i % FN] =
-        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i / FN], f.b[i % FN], acc[i / FN][i % FN], 0, 0, 0);
+    if constexpr (TRANSPOSED)
+      acc[i / FN][i % FN] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[i % FN], f.a[i / FN], acc[i / FN][i % FN], 0, 0, 0);
+    else
+      acc[i / FN][i % FN] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i / FN], f.b[i % FN], acc[i / FN][i % FN], 0, 0, 0);
   };
 
   using S0 = std::integral_constant<int, 0>;
@@ -546,11 +557,127 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
   // clamped tail loads may still be landing in LDS: drain before leaving
   vm_wait<0>();
 
-  // ---- epilogue, staged through the (now idle) LDS ring in two halves of
-  // 128 rows: waves of row-half h write t = bf16(acc) into padded rows
-  // (264 elements, so the two 32-lane row groups of a write hit opposite bank
-  // halves), then all 256 threads walk the half in 16-byte row chunks, apply
-  // bias / GELU / residual with vector loads and store 16 bytes at a time.
+  if constexpr (TRANSPOSED) {
+    // ---- bias + GELU in registers, then the tile through LDS for 16-byte
+    // row stores.  Lane l holds, per (fm, fn, q), the outputs (row
+    // fm*32 + l%32, columns fn*32 + 8q + 4*(l/32) .. +3) of its wave's block:
+    // bf16(acc) and bias in fp32, bf16 again, the paired table GELU (one wave
+    // vote per fm picks it, or the exact rules when a NaN, an infinity or a
+    // tiny magnitude is present), one 8-byte LDS write per 4 columns.  The
+    // 256 x 256 bf16 tile fills 8 ring arrays (32 rows of 512 B each, 16-byte
+    // chunk k of row r at k ^ (r % 32): a 16-lane read of one row's 16 chunks
+    // covers all 64 banks, a 32-row write two lanes per bank pair); the GELU
+    // table sits in a ninth array.
+    __shared__ __attribute__((aligned(16))) uint16_t TabX[STAGES > 4 ? 8 : GELU_TABLE_SIZE + 8];
+    uint16_t *tab_lds = STAGES > 4 ? As4 : TabX;
+    static_assert(GELU_TABLE_SIZE <= A_STAGE, "GELU table fits in one ring array");
+    auto stage_row = [&](int r) -> uint16_t * {
+      uint16_t *base;
+      switch (r >> 5) {
+        case 0: base = As0; break;
+        case 1: base = As1; break;
+        case 2: base = As2; break;
+        case 3: base = As3; break;
+        case 4: base = Bs0; break;
+        case 5: base = Bs1; break;
+        case 6: base = Bs2; break;
+        default: base = Bs3; break;
+      }
+      return base + (r & 31) * G2_BN;
+    };
+    __syncthreads();  // every wave is done reading the ring
+    for (int i = tid; i < (GELU_TABLE_SIZE + 1) / 2; i += NTHR)
+      reinterpret_cast<uint32_t *>(tab_lds)[i] = reinterpret_cast<const uint32_t *>(g.gelu_tab)[i];
+    const int gq = lane >> 5;
+    const int cw = wn * TN + 4 * gq;  // tile column of the lane's first output, + fn*32 + 8q
+    float bias_f[FN][4][4];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + cw + fn * 32 + 8 * q;
+        uint2 bw = {0u, 0u};
+        if (g.bias && n < g.N) bw = *reinterpret_cast<const uint2 *>(g.bias + n);
+        bias_f[fn][q][0] = lo_bf(bw.x);
+        bias_f[fn][q][1] = hi_bf(bw.x);
+        bias_f[fn][q][2] = lo_bf(bw.y);
+        bias_f[fn][q][3] = hi_bf(bw.y);
+      }
+    __syncthreads();  // the table is in LDS
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int r = wm * TM + fm * 32 + (lane & 31);
+      uint32_t u[FN][4][2], mg[FN][4][2];
+      GeluVote vote = gelu_vote_init();
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t t = pack_bf(acc[fm][fn][4 * q + 2 * h], acc[fm][fn][4 * q + 2 * h + 1]);
+            u[fn][q][h] = pack_bf(lo_bf(t) + bias_f[fn][q][2 * h], hi_bf(t) + bias_f[fn][q][2 * h + 1]);
+            mg[fn][q][h] = u[fn][q][h] & 0x7FFF7FFFu;
+            gelu_vote_add(vote, mg[fn][q][h]);
+          }
+      if (__builtin_amdgcn_ballot_w64(gelu_vote_special(vote)) == 0) {
+        GeluPairIdx t[FN][4][2];
+        uint32_t tl[FN][4][2], th[FN][4][2];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              t[fn][q][h] = gelu_pair_index(u[fn][q][h], mg[fn][q][h]);
+              tl[fn][q][h] = tab_lds[t[fn][q][h].idx & 0xFFFFu];
+              th[fn][q][h] = tab_lds[t[fn][q][h].idx >> 16];
+            }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              u[fn][q][h] = gelu_pair_finish(u[fn][q][h], mg[fn][q][h], t[fn][q][h].off,
+                                             tl[fn][q][h] | (th[fn][q][h] << 16));
+      } else {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) u[fn][q][h] = gelu_pair_exact(u[fn][q][h], tab_lds);
+      }
+      uint16_t *row = stage_row(r);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int k = (cw + fn * 32 + 8 * q) >> 3;
+          *reinterpret_cast<uint2 *>(row + 8 * (k ^ (r & 31)) + 4 * gq) = uint2{u[fn][q][0], u[fn][q][1]};
+        }
+    }
+    __syncthreads();
+    uint16_t *__restrict__ Cp = g.C;
+    constexpr int NC = G2_BM * (G2_BN / 8) / NTHR;  // 16-byte chunks per thread
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int qd = tid + j * NTHR;
+      const int r = qd >> 5, k = qd & 31;
+      const int m = m0 + r, n = n0 + 8 * k;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(stage_row(r) + 8 * (k ^ (r & 31)));
+      if (m < g.M && n < g.N) *reinterpret_cast<u32x4 *>(Cp + (size_t)m * g.N + n) = v;
+    }
+    return;
+  }
+
+  // ---- epilogue of the other forms, staged through the (now idle) LDS ring
+  // in two halves of 128 rows: waves of row-half h write t = bf16(acc) into
+  // padded rows (264 elements, so the two 32-lane row groups of a write hit
+  // opposite bank halves), then all threads walk the half in 16-byte row
+  // chunks, apply bias / residual with vector loads and store 16 bytes at a
+  // time.
   // 8-row block b of a half lives in ring array b / 3 at row offset (b % 3) * 8.
   constexpr int EP_LD = 264;
   auto ep_block = [&](int blk) -> uint16_t * {
@@ -564,29 +691,14 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
     }
   };
   __syncthreads();  // every wave is done reading the ring
-  // The epilogue's operands: the bias chunk of a thread's columns is the same
-  // for every row it visits (its column group is tid % 32), so it is loaded
-  // once; the GELU table is copied into ring array Bs2, which the staging
-  // below leaves unused, so each lookup is an LDS read instead of a global
-  // load whose latency every 8-element chunk would wait for.
+  // The bias chunk of a thread's columns is the same for every row it visits
+  // (its column group is tid % 32), so it is loaded once.
   uint16_t *__restrict__ Cp = g.C;
   const uint16_t *__restrict__ Rp = g.R;
   const int c_thr = tid & 31;
   u32x4 bv = {0, 0, 0, 0};
-  if constexpr (EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID)
+  if constexpr (EPI == EPI_BIAS_RESID)
     if (g.bias && n0 + 8 * c_thr < g.N) bv = *reinterpret_cast<const u32x4 *>(g.bias + n0 + 8 * c_thr);
-  float bias_f[8];
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    bias_f[2 * w] = lo_bf(bv[w]);
-    bias_f[2 * w + 1] = hi_bf(bv[w]);
-  }
-  uint16_t *tab_lds = Bs2;
-  if constexpr (EPI == EPI_BIAS_GELU) {
-    static_assert(GELU_TABLE_SIZE <= B_STAGE, "GELU table fits in one ring array");
-    for (int i = tid; i < (GELU_TABLE_SIZE + 1) / 2; i += NTHR)
-      reinterpret_cast<uint32_t *>(tab_lds)[i] = reinterpret_cast<const uint32_t *>(g.gelu_tab)[i];
-  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     if (wm / (WMN / 2) == h) {
@@ -607,69 +719,6 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
         }
     }
     __syncthreads();
-    if constexpr (EPI == EPI_BIAS_GELU) {
-      // The whole half at once: all NJ chunks of a thread are read and biased
-      // first, one wave vote picks the paired GELU (no NaN or infinity in the
-      // wave's half) or the exact per-element one for all of them, then every
-      // table lookup is issued before any result is stored.
-      uint32_t u[NJ][4];
-      uint32_t special = 0;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int r = (tid + j * NTHR) >> 5;
-        const u32x4 tv = *reinterpret_cast<const u32x4 *>(ep_block(r >> 3) + (r & 7) * EP_LD + 8 * c_thr);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          u[j][w] = pack_bf(lo_bf(tv[w]) + bias_f[2 * w], hi_bf(tv[w]) + bias_f[2 * w + 1]);
-          special |= gelu_pair_special(u[j][w]);
-        }
-      }
-      if (__builtin_amdgcn_ballot_w64(special != 0) == 0) {
-        // Table reads one chunk ahead: chunk j+1's indices and reads are
-        // issued before chunk j's results are formed, so each wait covers the
-        // LDS latency of four pairs rather than of one (GEMM1 shape: 482 ->
-        // 472 us; two chunks ahead measured the same).
-        constexpr int G = 1;  // chunks per group (4 pairs each)
-        GeluPairIdx t[2][G][4];
-        uint32_t tl[2][G][4], th[2][G][4];
-        auto fetch = [&](int b, int j0) __attribute__((always_inline)) {
-#pragma unroll
-          for (int jj = 0; jj < G; ++jj)
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              t[b][jj][w] = gelu_pair_index(u[j0 + jj][w]);
-              tl[b][jj][w] = tab_lds[t[b][jj][w].idx & 0xFFFFu];
-              th[b][jj][w] = tab_lds[t[b][jj][w].idx >> 16];
-            }
-        };
-        fetch(0, 0);
-#pragma unroll
-        for (int j0 = 0; j0 < NJ; j0 += G) {
-          const int b = (j0 / G) & 1;
-          if (j0 + G < NJ) fetch(b ^ 1, j0 + G);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int jj = 0; jj < G; ++jj)
-#pragma unroll
-            for (int w = 0; w < 4; ++w)
-              u[j0 + jj][w] = gelu_pair_finish(u[j0 + jj][w], t[b][jj][w].off, tl[b][jj][w] | (th[b][jj][w] << 16));
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) u[j][w] = gelu_pair_exact(u[j][w], tab_lds);
-      }
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int r = (tid + j * NTHR) >> 5;
-        const int m = m0 + h * 128 + r, n = n0 + 8 * c_thr;
-        if (m < g.M && n < g.N)
-          *reinterpret_cast<u32x4 *>(Cp + (size_t)m * g.N + n) = u32x4{u[j][0], u[j][1], u[j][2], u[j][3]};
-      }
-      if (h == 0) __syncthreads();  // the half is consumed before the next overwrites it
-      continue;
-    }
 #pragma unroll 4
     for (int j = 0; j < NJ; ++j) {
       const int qd = tid + j * NTHR;

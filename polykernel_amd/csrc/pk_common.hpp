@@ -209,7 +209,8 @@ typedef short pk_i16x2 __attribute__((ext_vector_type(2)));
 // The packed operations of gelu_pair_common as instructions: written as
 // vector-of-u16 C, the compiler turns the min/sub and arithmetic-shift masks
 // into per-half compares and selects; pinned, each is one instruction for both
-// halves (the pair takes 15 VALU instructions and two LDS reads).  Inline
+// halves (given the magnitudes, the pair takes 9 packed instructions, two LDS
+// reads and their two address computations, and one combine).  Inline
 // constants of packed ops fill only the low half, so op_sel_hi selects the low
 // half for both lanes.
 #pragma clang diagnostic push
@@ -254,6 +255,31 @@ __device__ __forceinline__ uint32_t pk_vbfi(uint32_t m, uint32_t a, uint32_t b) 
   asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
   return r;
 }
+__device__ __forceinline__ uint32_t pk_vbfi_s(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vlshr15_u16(uint32_t a) {
+  uint32_t r;
+  asm("v_pk_lshrrev_b16 %0, 15, %1 op_sel_hi:[0,1]" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vmad_u16s(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vsubsat_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "s"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_vmax_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_max_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 #pragma clang diagnostic pop
 // Nonzero when either code of the pair leaves gelu_pair_common's domain: a
 // NaN or an infinity (magnitude >= 0x7F80) or a nonzero magnitude below
@@ -267,32 +293,52 @@ __device__ __forceinline__ uint32_t gelu_pair_special(uint32_t w) {
   return ((nonzero & ~normal) | inf_nan) & 0x80008000u;
 }
 
+// The domain test of gelu_pair_special accumulated over many pairs with two
+// packed min/max instructions per pair: mn keeps the least (mag - 1) per half
+// (a zero magnitude wraps to 0xFFFF), mx the greatest magnitude.  Some code
+// left the domain exactly when a nonzero magnitude was below 0x0100
+// (mag - 1 < 0x00FF) or a magnitude reached 0x7F80.
+struct GeluVote {
+  uint32_t mn, mx;
+};
+__device__ __forceinline__ GeluVote gelu_vote_init() { return {0xFFFFFFFFu, 0u}; }
+// mag = w & 0x7FFF7FFF of the pair w.
+__device__ __forceinline__ void gelu_vote_add(GeluVote &v, uint32_t mag) {
+  v.mn = pk_vmin_u16(v.mn, pk_vsub_u16(mag, 0x00010001u));
+  v.mx = pk_vmax_u16(v.mx, mag);
+}
+__device__ __forceinline__ bool gelu_vote_special(const GeluVote &v) {
+  const uint32_t mn = min(v.mn & 0xFFFFu, v.mn >> 16), mx = max(v.mx & 0xFFFFu, v.mx >> 16);
+  return mn < 0x00FFu || mx >= 0x7F80u;
+}
+
 // gelu_pair_common in two steps, so that a caller can issue the table reads of
 // many pairs before it needs any of them: the table index of both codes (and
-// the clamped offsets, which mark |x| < TLO), then the result from the two
-// table values.
+// the offsets mag - TLO, whose sign bit marks |x| < TLO), then the result from
+// the two table values.  mag = w & 0x7FFF7FFF is shared with gelu_vote_add.
 struct GeluPairIdx {
   uint32_t off, idx;
 };
-__device__ __forceinline__ GeluPairIdx gelu_pair_index(uint32_t w) {
+__device__ __forceinline__ GeluPairIdx gelu_pair_index(uint32_t w, uint32_t mag) {
   constexpr uint32_t TLO2 = GELU_TLO | (GELU_TLO << 16);
   constexpr uint32_t CLAMP2 = (uint32_t)GELU_SPAN | ((uint32_t)GELU_SPAN << 16);  // sentinel slot
   constexpr uint32_t HALF2 = (uint32_t)GELU_HALF | ((uint32_t)GELU_HALF << 16);
-  const uint32_t sgn = pk_vasr15_i16(w);                 // 0xFFFF per negative half
-  const uint32_t off = pk_vsub_u16(w & 0x7FFF7FFFu, TLO2);
-  return {off, pk_vadd_u16v(pk_vmin_u16s(off, CLAMP2), sgn & HALF2)};
+  const uint32_t off = pk_vsub_u16(mag, TLO2);
+  // (sign bit) * HALF + min(off, SPAN): at most 2 * SPAN + 1 < 65536
+  return {off, pk_vmad_u16s(pk_vlshr15_u16(w), HALF2, pk_vmin_u16s(off, CLAMP2))};
 }
-__device__ __forceinline__ uint32_t gelu_pair_finish(uint32_t w, uint32_t off, uint32_t tv) {
+__device__ __forceinline__ uint32_t gelu_pair_finish(uint32_t w, uint32_t mag, uint32_t off, uint32_t tv) {
   const uint32_t r = pk_vmin_u16(tv, w);                 // table value, or x / -0 above it
-  // exponent field - 1 (signed saturation keeps -0; the max keeps +0)
-  const uint32_t half = pk_vmax_i16(pk_vsubsat_i16(w, 0x00800080u), w & 0x80008000u);
+  // exponent field - 1: the magnitude less 0x80, saturating at 0, with the sign of x
+  const uint32_t half = pk_vbfi_s(0x7FFF7FFFu, pk_vsubsat_u16(mag, 0x00800080u), w);
   const uint32_t m_small = pk_vasr15_i16(off);           // 0xFFFF where |x| < TLO
   return pk_vbfi(m_small, half, r);
 }
 __device__ __forceinline__ uint32_t gelu_pair_common(uint32_t w, const uint16_t *__restrict__ tab) {
-  const GeluPairIdx t = gelu_pair_index(w);
+  const uint32_t mag = w & 0x7FFF7FFFu;
+  const GeluPairIdx t = gelu_pair_index(w, mag);
   const uint32_t tv = (uint32_t)tab[t.idx & 0xFFFFu] | ((uint32_t)tab[t.idx >> 16] << 16);
-  return gelu_pair_finish(w, t.off, tv);
+  return gelu_pair_finish(w, mag, t.off, tv);
 }
 
 // Both codes of a pair through the exact per-element rules.
