@@ -479,6 +479,31 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
   using S3 = std::integral_constant<int, 3>;
   using S4 = std::integral_constant<int, 4>;
 
+  // The GELU epilogue's operands are loaded before the first DMA, so their
+  // latency hides behind the main loop instead of opening the epilogue: this
+  // thread's words of the GELU table (copied into LDS once the ring is free)
+  // and the bias of the lane's 32 columns.  Issued ahead of every DMA load,
+  // they are older than all of them, so the in-order vmcnt waits below still
+  // count only DMA loads behind them.
+  constexpr int TAB_W = (GELU_TABLE_SIZE + 1) / 2;  // table words
+  constexpr int TAB_PT = (TAB_W + NTHR - 1) / NTHR;
+  uint32_t tab_pre[TRANSPOSED ? TAB_PT : 1];
+  uint2 bias_pre[TRANSPOSED ? FN * 4 : 1];
+  if constexpr (TRANSPOSED) {
+#pragma unroll
+    for (int j = 0; j < TAB_PT; ++j) {
+      const int i = tid + j * NTHR;
+      tab_pre[j] = i < TAB_W ? reinterpret_cast<const uint32_t *>(g.gelu_tab)[i] : 0u;
+    }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * TN + 4 * (lane >> 5) + fn * 32 + 8 * q;
+        bias_pre[fn * 4 + q] = (g.bias && n < g.N) ? *reinterpret_cast<const uint2 *>(g.bias + n) : uint2{0u, 0u};
+      }
+  }
+
   // ---- prologue: tiles 0..STAGES-2 and the A half of tile STAGES-1 in
   // flight (indices past the end are clamped to the last tile: every k-tile
   // issues the same number of DMA loads, so each wait below is a compile-time
@@ -586,8 +611,9 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
       return base + (r & 31) * G2_BN;
     };
     __syncthreads();  // every wave is done reading the ring
-    for (int i = tid; i < (GELU_TABLE_SIZE + 1) / 2; i += NTHR)
-      reinterpret_cast<uint32_t *>(tab_lds)[i] = reinterpret_cast<const uint32_t *>(g.gelu_tab)[i];
+#pragma unroll
+    for (int j = 0; j < TAB_PT; ++j)
+      if (tid + j * NTHR < TAB_W) reinterpret_cast<uint32_t *>(tab_lds)[tid + j * NTHR] = tab_pre[j];
     const int gq = lane >> 5;
     const int cw = wn * TN + 4 * gq;  // tile column of the lane's first output, + fn*32 + 8q
     float bias_f[FN][4][4];
@@ -595,9 +621,7 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
     for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + cw + fn * 32 + 8 * q;
-        uint2 bw = {0u, 0u};
-        if (g.bias && n < g.N) bw = *reinterpret_cast<const uint2 *>(g.bias + n);
+        const uint2 bw = bias_pre[fn * 4 + q];
         bias_f[fn][q][0] = lo_bf(bw.x);
         bias_f[fn][q][1] = hi_bf(bw.x);
         bias_f[fn][q][2] = lo_bf(bw.y);
