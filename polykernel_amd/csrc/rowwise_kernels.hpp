@@ -108,6 +108,18 @@ __device__ __forceinline__ void rmsnorm_vec_body(const RowArgs &a) {
   const int nvec = cols >> 3;
   const size_t base = (size_t)row * cols;
 
+  // Every load of the row (and residual) is issued before the first is
+  // unpacked ([4096, 4096] + gamma 14.05 -> 13.55 us, residual + RMSNorm
+  // [16384, 8192] 126.7 -> 124.1 us, bit-identical).
+  U4 xw[VPT], rw[RESID ? VPT : 1];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = lane + i * kLanes;
+    if (c < nvec) {
+      xw[i] = ld16_once(x + base + (size_t)c * 8);
+      if constexpr (RESID) rw[i] = ld16_once(r + base + (size_t)c * 8);
+    }
+  }
   float v[VPT][8];
   float ss = 0.f;
   DivSpan span;  // magnitudes of the numerators (without a residual: the loaded words)
@@ -115,17 +127,16 @@ __device__ __forceinline__ void rmsnorm_vec_body(const RowArgs &a) {
   for (int i = 0; i < VPT; ++i) {
     const int c = lane + i * kLanes;
     if (c < nvec) {
-      const U4 xw = ld16_once(x + base + (size_t)c * 8);
-      unpack8(xw, v[i]);
+      unpack8(xw[i], v[i]);
       if constexpr (!RESID) {
-        div_span_add(span, xw.x);
-        div_span_add(span, xw.y);
-        div_span_add(span, xw.z);
-        div_span_add(span, xw.w);
+        div_span_add(span, xw[i].x);
+        div_span_add(span, xw[i].y);
+        div_span_add(span, xw[i].z);
+        div_span_add(span, xw[i].w);
       }
       if constexpr (RESID) {
         float rv[8];
-        unpack8(ld16_once(r + base + (size_t)c * 8), rv);
+        unpack8(rw[i], rv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[i][e] = bf2f(f2bf(v[i][e] + rv[e]));
       }
@@ -208,20 +219,42 @@ __device__ __forceinline__ void rmsnorm_generic_body(const RowArgs &a) {
 // MODE 1: fp32 logits + bf16 additive mask, z = bf16(bf16(x) + mask)
 // (tests/golden/golden.py:115-117).  m = max z, e = exp(z - m), y = bf16(e * (1/sum e)).
 // ---------------------------------------------------------------------------
+// The words of 8 consecutive inputs (MODE 0: 8 bf16 in a; MODE 1: 8 fp32 in
+// a, b and 8 bf16 mask values in mk) and the softmax input z they give.
 template <int MODE>
-__device__ __forceinline__ void load_z8(const void *in, const uint16_t *mask, size_t off,
-                                        float (&z)[8]) {
+struct Z8Words {
+  U4 a, b, mk;
+};
+template <int MODE>
+__device__ __forceinline__ Z8Words<MODE> load_z8_words(const void *in, const uint16_t *mask, size_t off) {
+  Z8Words<MODE> w;
   if constexpr (MODE == 0) {
-    unpack8(ld16_once(static_cast<const uint16_t *>(in) + off), z);
+    w.a = ld16_once(static_cast<const uint16_t *>(in) + off);
   } else {
     const float *xf = static_cast<const float *>(in) + off;
-    const U4 a = ld16_once(xf), b = ld16_once(xf + 4);
+    w.a = ld16_once(xf);
+    w.b = ld16_once(xf + 4);
+    w.mk = ld16_once(mask + off);
+  }
+  return w;
+}
+template <int MODE>
+__device__ __forceinline__ void z8_of(const Z8Words<MODE> &w, float (&z)[8]) {
+#pragma clang fp contract(off)
+  if constexpr (MODE == 0) {
+    unpack8(w.a, z);
+  } else {
     float m[8];
-    unpack8(ld16_once(mask + off), m);
-    const uint32_t raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    unpack8(w.mk, m);
+    const uint32_t raw[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) z[e] = bf2f(f2bf(bf2f(f2bf(__uint_as_float(raw[e]))) + m[e]));
   }
+}
+template <int MODE>
+__device__ __forceinline__ void load_z8(const void *in, const uint16_t *mask, size_t off,
+                                        float (&z)[8]) {
+  z8_of<MODE>(load_z8_words<MODE>(in, mask, off), z);
 }
 
 template <int MODE>
@@ -250,13 +283,20 @@ __device__ __forceinline__ void softmax_vec_body(const RowArgs &a) {
   const int nvec = cols >> 3;
   const size_t base = (size_t)row * cols;
 
+  // every load of the row before the first conversion, as in rmsnorm_vec_body
+  Z8Words<MODE> zw[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = lane + i * kLanes;
+    if (c < nvec) zw[i] = load_z8_words<MODE>(in, mask, base + (size_t)c * 8);
+  }
   float z[VPT][8];
   float m = -INFINITY;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = lane + i * kLanes;
     if (c < nvec) {
-      load_z8<MODE>(in, mask, base + (size_t)c * 8, z[i]);
+      z8_of<MODE>(zw[i], z[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) m = fmaxf(m, z[i][e]);
     }
