@@ -217,7 +217,7 @@ __device__ __forceinline__ void att_body(AttArgs g) {
         s[kb][i] = v;
         tmax = fmaxf(tmax, v);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = xor32_max(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     const float alpha = __expf(m_run - m_use);
@@ -238,7 +238,7 @@ __device__ __forceinline__ void att_body(AttArgs g) {
         phi[kb][i >> 1] = h0 | (h1 << 16);
         plo[kb][i >> 1] = l0 | (l1 << 16);
       }
-    psum += __shfl_xor(psum, 32, 64);
+    psum = xor32_sum(psum);
     l_run = l_run * alpha + psum;
     m_run = m_new;
 #pragma unroll
@@ -446,7 +446,7 @@ __device__ __forceinline__ void att_wide_body(AttArgs g) {
       s[i] = v;
       tmax = fmaxf(tmax, v);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = xor32_max(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     const float alpha = __expf(m_run - m_use);
@@ -463,7 +463,7 @@ __device__ __forceinline__ void att_wide_body(AttArgs g) {
       phi[i >> 1] = h0 | (h1 << 16);
       plo[i >> 1] = l0 | (l1 << 16);
     }
-    psum += __shfl_xor(psum, 32, 64);
+    psum = xor32_sum(psum);
     l_run = l_run * alpha + psum;
     m_run = m_new;
 #pragma unroll
@@ -747,7 +747,7 @@ __device__ __forceinline__ void fa_body(FaArgs g) {
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) m = fmaxf(m, x[i]);
-    return fmaxf(m, __shfl_xor(m, 32, 64));
+    return xor32_max(m);
   };
   // pre_max: the block's row max when the caller has it (unmasked blocks)
   auto softmax = [&](auto mask_c, int step, f32x16 sc, Pw &pw, bool &resc, const float *pre_max = nullptr)
@@ -765,7 +765,7 @@ __device__ __forceinline__ void fa_body(FaArgs g) {
         }
         tmax = fmaxf(tmax, sc[i]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = xor32_max(tmax);
     }
     float alpha = 1.f;
     resc = __any((tmax - m_run) * c2 > 8.0f);  // also true for the first block (m_run = -inf)
@@ -786,7 +786,7 @@ __device__ __forceinline__ void fa_body(FaArgs g) {
       phi[i >> 1] = hh;
       plo[i >> 1] = pack_bf(p0 - lo_bf(hh), p1 - hi_bf(hh));
     }
-    psum += __shfl_xor(psum, 32, 64);
+    psum = xor32_sum(psum);
     l_run = l_run * alpha + psum;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {

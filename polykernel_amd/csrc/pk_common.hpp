@@ -426,4 +426,25 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// In every lane l, the values of lanes l % 32 and l % 32 + 32 (lo, hi), from
+// one v_permlane32_swap_b32 (that lane layout was checked on the device)
+// instead of an LDS permute.  xor32_max / xor32_sum combine a value with the
+// one of lane l ^ 32; max and + are commutative, so the result is the same
+// as fmaxf(v, shfl_xor(v, 32)) / v + shfl_xor(v, 32) and equal in both lanes.
+__device__ __forceinline__ void xor32_pair(float v, float &lo, float &hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  float lo, hi;
+  xor32_pair(v, lo, hi);
+  return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  float lo, hi;
+  xor32_pair(v, lo, hi);
+  return lo + hi;
+}
+
 }  // namespace pk
