@@ -129,15 +129,17 @@ __device__ __forceinline__ void reduce8_body(const float *partial, int splits, i
 //     cycles); odd NT needs none.
 //   A part: [16*MT rows][8 chunks of 16 B] bf16 (64 k), slot s of row r holds
 //     chunk s ^ (r & 7) (each wave loads its own copy from L2).
-// ds_read_b64_tr_b8 turns 8 rows x 16 columns of int8 into the MFMA B
-// operand (lane j of a 16-lane group receives column j, rows 0..7 -- checked
-// on the device); the 8 bytes are widened to bf16 exactly
-// (v_cvt_f32_i32 with a sign-extending byte select, then v_cvt_pk_bf16_f32)
-// and fed to v_mfma_f32_16x16x32_bf16 with A from a ds_read_b128.
-// Every step issues the same number of DMA loads, so each wait is a constant
-// vmcnt.  The epilogue (scale, bf16, GELU / residual, or fp32 partials for
-// the split reduction) goes through the wave's own LDS region, one m-tile at
-// a time, with 16-byte global accesses.
+// ds_read_b64_tr_b8 turns 8 rows x 16 columns of int8 into an MFMA operand
+// (lane j of a 16-lane group receives column j, rows 0..7 -- checked on the
+// device); the 8 bytes are widened to bf16 exactly (v_cvt_f32_i32 with a
+// sign-extending byte select, then v_cvt_pk_bf16_f32) and fed, as the first
+// operand, to v_mfma_f32_16x16x32_bf16 with the activations (a ds_read_b128)
+// as the second, so each lane's accumulators are 4 consecutive columns of one
+// row.  Every step issues the same number of DMA loads, so each wait is a
+// constant vmcnt.  Split partials are stored from those registers with
+// 16-byte stores; the final epilogue (scale, bf16, GELU / residual) goes
+// through the wave's own LDS region, one m-tile at a time, with 16-byte
+// global accesses.
 constexpr int I8S_KSTEP = 64;
 // Config fields fixed by the kernel's design: int8 elements per 16-byte DMA
 // lane, and 16x16x32 MFMA k-steps per 64-row ring step.
@@ -174,8 +176,8 @@ __device__ __forceinline__ void stream_body(const I8sArgs &g) {
   constexpr int P = NT + 2 * MT;           // DMA instructions per step
   constexpr int WN = 16 * NT;              // columns per wave
   constexpr int NB = WAVES * WN;           // columns per workgroup
-  // the epilogue buffer [16][WN] fp32 reuses the wave's region of stage 0
-  static_assert(16 * WN * 4 <= STAGE, "epilogue buffer");
+  // the epilogue buffer [16][WN + 4] fp32 reuses the wave's region of stage 0
+  static_assert(16 * (WN + 4) * 4 <= STAGE, "epilogue buffer");
   __shared__ __attribute__((aligned(1024))) uint8_t R0[WAVES * STAGE], R1[WAVES * STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t R2[STAGES > 2 ? WAVES * STAGE : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t R3[STAGES > 3 ? WAVES * STAGE : 16];
@@ -277,7 +279,7 @@ __device__ __forceinline__ void stream_body(const I8sArgs &g) {
         const bf16x8 b = widen8(w);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], b, acc[mt][j], 0, 0, 0);
+          acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[mt], acc[mt][j], 0, 0, 0);
       }
     }
   };
@@ -332,39 +334,50 @@ __device__ __forceinline__ void stream_body(const I8sArgs &g) {
     vm_wait<0>();
     for (; t < T; ++t) dispatch(t % STAGES, [&](auto c) __attribute__((always_inline)) { compute(c); });
 
-    // ---- epilogue, one m-tile at a time through this wave's region of stage 0:
-    // buf[16][WN] fp32, then 8 columns per item with 16-byte accesses.
-    float *buf = reinterpret_cast<float *>(R0 + wid * STAGE);
+    // ---- epilogue.  The product is formed transposed (the widened weights are
+    // the MFMA's first operand; the same exact products in the same k order),
+    // so lane l holds, per (mt, j), the 4 consecutive columns
+    // 16j + 4*(l/16) .. +3 of row 16mt + l%16.  Split partials go straight to
+    // memory as 16-byte stores; the final epilogue goes one m-tile at a time
+    // through this wave's region of stage 0 (buf[16][WN + 4] fp32: the 16 rows
+    // of a 16-byte write fall on distinct bank quads), then 8 columns per item.
     lgkm_wait0();
+    if (g.splits > 1) {
   #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = m0 + 16 * mt + gi;
   #pragma unroll
-      for (int j = 0; j < NT; ++j)
-  #pragma unroll
-        for (int i = 0; i < 4; ++i) buf[(4 * grp + i) * WN + 16 * j + gi] = acc[mt][j][i];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      constexpr int ITEMS = 16 * (WN / 8);
-  #pragma unroll
-      for (int it0 = 0; it0 < ITEMS; it0 += 64) {
-        const int it = it0 + lane;
-        if (ITEMS % 64 != 0 && it >= ITEMS) break;
-        const int r = it / (WN / 8), c8 = it % (WN / 8);
-        const int m = m0 + 16 * mt + r, n = n0 + 8 * c8;
-        if (m >= g.M || n >= g.N) continue;
-        const f32x4 v0 = *reinterpret_cast<const f32x4 *>(buf + r * WN + 8 * c8);
-        const f32x4 v1 = *reinterpret_cast<const f32x4 *>(buf + r * WN + 8 * c8 + 4);
-        if (g.splits > 1) {
-          float *dst = g.partial + ((size_t)split * g.M + m) * g.N + n;
-          *reinterpret_cast<f32x4 *>(dst) = v0;
-          *reinterpret_cast<f32x4 *>(dst + 4) = v1;
-          continue;
+        for (int j = 0; j < NT; ++j) {
+          const int n = n0 + 16 * j + 4 * grp;
+          if (m < g.M && n < g.N)
+            *reinterpret_cast<f32x4 *>(g.partial + ((size_t)split * g.M + m) * g.N + n) = acc[mt][j];
         }
-        int8_epilogue8<EPI>(v0, v1, m, n, g.N, g.scale, g.R, g.gelu_tab, g.C);
+      }
+    } else {
+      constexpr int LD = WN + 4;
+      float *buf = reinterpret_cast<float *>(R0 + wid * STAGE);
+  #pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  #pragma unroll
+        for (int j = 0; j < NT; ++j) *reinterpret_cast<f32x4 *>(buf + gi * LD + 16 * j + 4 * grp) = acc[mt][j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        constexpr int ITEMS = 16 * (WN / 8);
+  #pragma unroll
+        for (int it0 = 0; it0 < ITEMS; it0 += 64) {
+          const int it = it0 + lane;
+          if (ITEMS % 64 != 0 && it >= ITEMS) break;
+          const int r = it / (WN / 8), c8 = it % (WN / 8);
+          const int m = m0 + 16 * mt + r, n = n0 + 8 * c8;
+          if (m >= g.M || n >= g.N) continue;
+          const f32x4 v0 = *reinterpret_cast<const f32x4 *>(buf + r * LD + 8 * c8);
+          const f32x4 v1 = *reinterpret_cast<const f32x4 *>(buf + r * LD + 8 * c8 + 4);
+          int8_epilogue8<EPI>(v0, v1, m, n, g.N, g.scale, g.R, g.gelu_tab, g.C);
+        }
       }
     }
   }
