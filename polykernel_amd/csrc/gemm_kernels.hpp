@@ -590,9 +590,9 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
     // vote per fm picks it, or the exact rules when a NaN, an infinity or a
     // tiny magnitude is present), one 8-byte LDS write per 4 columns.  The
     // 256 x 256 bf16 tile fills 8 ring arrays (32 rows of 512 B each, 16-byte
-    // chunk k of row r at k ^ (r % 32): a 16-lane read of one row's 16 chunks
-    // covers all 64 banks, a 32-row write two lanes per bank pair); the GELU
-    // table sits in a ninth array.
+    // chunk k of row r at k ^ (r % 32), its two 8-byte halves swapped in rows
+    // 16-31: a 16-lane read of one row's 16 chunks and a 32-row write both
+    // cover all 64 banks once); the GELU table sits in a ninth array.
     __shared__ __attribute__((aligned(16))) uint16_t TabX[STAGES > 4 ? 8 : GELU_TABLE_SIZE + 8];
     uint16_t *tab_lds = STAGES > 4 ? As4 : TabX;
     static_assert(GELU_TABLE_SIZE <= A_STAGE, "GELU table fits in one ring array");
@@ -679,7 +679,8 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int k = (cw + fn * 32 + 8 * q) >> 3;
-          *reinterpret_cast<uint2 *>(row + 8 * (k ^ (r & 31)) + 4 * gq) = uint2{u[fn][q][0], u[fn][q][1]};
+          *reinterpret_cast<uint2 *>(row + 8 * (k ^ (r & 31)) + 4 * (gq ^ ((r >> 4) & 1))) =
+              uint2{u[fn][q][0], u[fn][q][1]};
         }
     }
     __syncthreads();
@@ -690,7 +691,11 @@ __device__ __forceinline__ void gemm_dma_body(GemmArgs g) {
       const int qd = tid + j * NTHR;
       const int r = qd >> 5, k = qd & 31;
       const int m = m0 + r, n = n0 + 8 * k;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(stage_row(r) + 8 * (k ^ (r & 31)));
+      u32x4 v = *reinterpret_cast<const u32x4 *>(stage_row(r) + 8 * (k ^ (r & 31)));
+      // rows 16-31 of each 32-row array hold their 8-byte halves swapped; the
+      // rows this j reads, (tid >> 5) + j * NTHR / 32, all fall on one side
+      static_assert(NTHR / 32 == 8 || NTHR / 32 == 16, "row step of the read-back");
+      if (((j * (NTHR / 32)) >> 4) & 1) v = u32x4{v[2], v[3], v[0], v[1]};
       if (m < g.M && n < g.N) *reinterpret_cast<u32x4 *>(Cp + (size_t)m * g.N + n) = v;
     }
     return;
