@@ -385,6 +385,28 @@ def test_fused_matmul_bias_gelu_integer_bit_exact(gpu, oracle, tile):
 
 
 @pytest.mark.parametrize("tile", [0, 3])
+def test_fused_matmul_bias_gelu_special_values_bit_exact(gpu, oracle, tile):
+    # Rows of A that are all zero make bf16(bf16(acc) + bias) the bias itself, so the bias
+    # row puts every special code through the epilogue: infinities, NaN, zeros of both
+    # signs, the exponent-0/1 magnitudes the paired GELU hands to the per-element rules,
+    # the largest finite values and the table edges.  The blocks that hold them take the
+    # exact per-element path, the other blocks of the same launch the paired one.
+    M, N, Kd = 512, 520, 96
+    a, b = int_bf16((M, Kd), 36), int_bf16((Kd, N), 37)
+    a[100:164] = 0
+    a[480:] = 0
+    bias = bf(np.random.default_rng(38).integers(-4, 5, size=N)).view(np.uint16).copy()
+    special = [0x7F80, 0xFF80, 0x7FC0, 0xFFC0, 0x0000, 0x8000, 0x0001, 0x8001, 0x007F, 0x0080,
+               0x80FF, 0x0100, 0x7F7F, 0xFF7F, 0x3B4A, 0x3B4B, 0xBB4B, 0x4031, 0x4032, 0xC0B1, 0xC0B2]
+    cols = np.random.default_rng(39).choice(N, size=4 * len(special), replace=False)
+    bias[cols] = np.tile(np.array(special, dtype=np.uint16), 4)
+    bias = bias.view(a.dtype)
+    got = from_dev(K().gemm_ex(1, to_dev(a), to_dev(b), bias=to_dev(bias), tile=tile))
+    want = oracle.fused_matmul_bias_gelu(a, b, bias)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("tile", [0, 3])
 def test_fused_matmul_bias_residual_integer_bit_exact(gpu, oracle, tile):
     a, b = int_bf16((600, 384), 32), int_bf16((384, 520), 33)
     bias = bf(np.random.default_rng(34).integers(-4, 5, size=520))
