@@ -453,3 +453,97 @@ def test_code_object_int8_launcher_rejects_null_operands():
         with pytest.raises(rt.RuntimeError_) as ei:
             r.run("matmul_int8_gelu", 16, 28672, 8192, io)
         assert "null tensor pointer" in ei.value.message, ei.value.message
+
+
+# ---- code-object launchers: refusals before any device call -----------------------
+# Each launcher served from an emitted code object checks its argument block the
+# way the linked path does (null operands, the entry's shape, the operand alignment
+# its config needs, a cached binary) before it loads a module or launches, so these
+# run without a GPU.  Pointers are fake, nonzero addresses: nothing dereferences them.
+
+GEMM_DMA = {"block_m": 256, "block_n": 256, "block_k": 32, "num_warps": 8,
+            "vector_width": 8, "unroll": 2, "shared_memory_stages": 5}
+PANEL = {"block_m": 32, "block_n": 64, "block_k": 768, "num_warps": 8,
+         "vector_width": 8, "unroll": 48, "shared_memory_stages": 1}
+ROW = {"block_m": 1, "block_n": 8192, "block_k": 0, "num_warps": 4,
+       "vector_width": 8, "unroll": 4, "shared_memory_stages": 1}
+FLASH = {"block_m": 64, "block_n": 128, "block_k": 128, "num_warps": 8,
+         "vector_width": 8, "unroll": 8, "shared_memory_stages": 2}
+
+
+def _object_runtime(op, shape, best):
+    c = rt.KernelCache()
+    e = entry(op=op, shape=dict(shape, dtype=rt.op_dtype(op)))
+    e["best"] = dict(best)
+    c.put(e)
+    return rt.Runtime(c, fixed_arch="gfx950", code_objects=True)
+
+
+def _refused(r, op, mnk, io, fragment):
+    with pytest.raises(rt.RuntimeError_) as ei:
+        r.run(op, *mnk, io)
+    assert fragment in ei.value.message, ei.value.message
+
+
+@pytest.mark.parametrize("op,needs", [("matmul", ("A", "B", "C")),
+                                      ("fused_matmul_bias_gelu", ("A", "B", "C", "bias")),
+                                      ("fused_matmul_bias_residual", ("A", "B", "C", "residual"))])
+def test_code_object_gemm_launcher_refusals(op, needs):
+    mnk = (512, 512, 256)
+    r = _object_runtime(op, dict(M=512, N=512, K=256), GEMM_DMA)
+    ok = dict(A=4096, B=8192, C=12288, bias=16384, residual=20480, M=512, N=512, K=256)
+    for missing in needs:
+        io = rt.MatmulIO(**ok)
+        setattr(io, missing, None)
+        _refused(r, op, mnk, io, "code object: null tensor pointer")
+    _refused(r, op, mnk, rt.MatmulIO(**dict(ok, K=128)), "does not match the selected entry")
+    _refused(r, op, mnk, rt.MatmulIO(**dict(ok, A=4098)), "needs 16-byte aligned A and B")
+    _refused(r, op, mnk, rt.MatmulIO(**dict(ok, C=12290)), "needs 16-byte aligned C, residual and bias")
+    # every check passed: the cache holds no binary for the entry
+    _refused(r, op, mnk, rt.MatmulIO(**ok), "no code object cached")
+
+
+def test_code_object_panel_launcher_refusals():
+    op, mnk = "fused_rmsnorm_matmul", (128, 3072, 768)
+    r = _object_runtime(op, dict(M=128, N=3072, K=768), PANEL)
+    ok = dict(x=4096, gamma=8192, W=12288, out=16384, M=128, N=3072, K=768, eps=1e-6)
+    for missing in ("x", "W", "out"):
+        io = rt.RmsnormMatmulIO(**ok)
+        setattr(io, missing, None)
+        _refused(r, op, mnk, io, "code object: null tensor pointer")
+    _refused(r, op, mnk, rt.RmsnormMatmulIO(**dict(ok, N=2048)), "does not match the selected entry")
+    _refused(r, op, mnk, rt.RmsnormMatmulIO(**dict(ok, gamma=8194)), "needs 16-byte aligned x, W, gamma and out")
+    _refused(r, op, mnk, rt.RmsnormMatmulIO(**ok), "no code object cached")
+
+
+def test_code_object_row_launcher_refusals():
+    rows, cols = 16384, 8192
+    r = _object_runtime("fused_residual_rmsnorm", dict(M=rows, N=cols, K=0), ROW)
+    ok = dict(x=4096, r=8192, gamma=12288, out=16384, rows=rows, cols=cols, eps=1e-6)
+    for missing in ("x", "r", "out"):
+        io = rt.ResidualRmsnormIO(**ok)
+        setattr(io, missing, None)
+        _refused(r, "fused_residual_rmsnorm", (rows, cols, 0), io, "code object: null tensor pointer")
+    _refused(r, "fused_residual_rmsnorm", (rows, cols, 0), rt.ResidualRmsnormIO(**dict(ok, cols=4096)),
+             "does not match the selected entry")
+    _refused(r, "fused_residual_rmsnorm", (rows, cols, 0), rt.ResidualRmsnormIO(**ok), "no code object cached")
+    r = _object_runtime("fused_softmax_mask", dict(M=rows, N=cols, K=0), dict(ROW, num_warps=8, unroll=2))
+    ok = dict(logits=4096, mask=8192, out=16384, rows=rows, cols=cols)
+    for missing in ("logits", "mask", "out"):
+        io = rt.SoftmaxMaskIO(**ok)
+        setattr(io, missing, None)
+        _refused(r, "fused_softmax_mask", (rows, cols, 0), io, "code object: null tensor pointer")
+    _refused(r, "fused_softmax_mask", (rows, cols, 0), rt.SoftmaxMaskIO(**ok), "no code object cached")
+
+
+def test_code_object_attention_launcher_refusals():
+    op, mnk = "fused_kv_append_attention", (512, 4096, 128)
+    r = _object_runtime(op, dict(M=512, N=4096, K=128), FLASH)
+    ok = dict(Q=4096, Kc=8192, Vc=12288, Kn=16384, Vn=20480, O=24576, B=1, H=32, S_q=512, S_cache=3584,
+              D=128, cache_capacity=4096, scale=0.088, causal=1)
+    for missing in ("Q", "Kc", "Vc", "Kn", "Vn", "O"):
+        io = rt.KvAppendAttentionIO(**ok)
+        setattr(io, missing, None)
+        _refused(r, op, mnk, io, "code object: null tensor pointer")
+    _refused(r, op, mnk, rt.KvAppendAttentionIO(**dict(ok, S_cache=3072)), "does not match the selected entry")
+    _refused(r, op, mnk, rt.KvAppendAttentionIO(**ok), "no code object cached")
