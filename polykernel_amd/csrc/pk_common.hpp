@@ -220,11 +220,6 @@ __device__ __forceinline__ uint32_t pk_vsub_u16(uint32_t a, uint32_t b) {
   asm("v_pk_sub_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
   return r;
 }
-__device__ __forceinline__ uint32_t pk_vadd_u16v(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_pk_add_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
 __device__ __forceinline__ uint32_t pk_vmin_u16(uint32_t a, uint32_t b) {
   uint32_t r;
   asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
@@ -233,16 +228,6 @@ __device__ __forceinline__ uint32_t pk_vmin_u16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t pk_vmin_u16s(uint32_t a, uint32_t b) {
   uint32_t r;
   asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
-  return r;
-}
-__device__ __forceinline__ uint32_t pk_vsubsat_i16(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_pk_sub_i16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "s"(b));
-  return r;
-}
-__device__ __forceinline__ uint32_t pk_vmax_i16(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_pk_max_i16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
 __device__ __forceinline__ uint32_t pk_vasr15_i16(uint32_t a) {
