@@ -61,10 +61,15 @@ def dev_bf16(a):
     return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
 
 
-def event_pair():
+def event_pair(fence: bool = False):
+    """Two timing events: TimingEvent (no cache maintenance at record) unless
+    `fence`, for timings that must start from written-back caches (the
+    MALL-flushed launches)."""
     import torch
 
-    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if fence:
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    return TimingEvent(), TimingEvent()
 
 
 class TimingEvent:
@@ -102,10 +107,13 @@ class TimingEvent:
         if rc != 0:
             raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
 
-    def record(self, stream) -> None:
+    def record(self, stream=None) -> None:
         import ctypes as C
 
-        rc = self._lib().hipEventRecord(self.h, C.c_void_p(stream.cuda_stream))
+        import torch
+
+        st = (stream or torch.cuda.current_stream()).cuda_stream
+        rc = self._lib().hipEventRecord(self.h, C.c_void_p(st))
         if rc != 0:
             raise RuntimeError(f"hipEventRecord failed ({rc})")
 
@@ -265,7 +273,7 @@ class Timer:
             per_s = max(e0.elapsed_time(e1) * 1e-3, 1e-6)
             for _ in range(min(int(warm_s / per_s) + 1, 20000)):
                 fn()
-        evs = [event_pair() for _ in range(n)]
+        evs = [event_pair(fence=flush is not None) for _ in range(n)]
         for e0, e1 in evs:
             if flush is not None:
                 flush()
