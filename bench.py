@@ -758,7 +758,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(the kernels run on one MI355X; see DESIGN.md for how the path would shard)",
+              "(the kernels run on one MI355X: token rows, attention heads and int8 weight "
+              "columns are the units a multi-GPU run would split)",
               file=sys.stderr, flush=True)
         return 2
 
