@@ -234,3 +234,67 @@ def test_rmsnorm_matmul_panel_in_a_replayed_graph(gpu):
         assert torch.equal(o.view(torch.int16), eager.view(torch.int16)), rep
         assert launch(eager, torch.cuda.current_stream().cuda_stream) == 0  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_mlp_block_and_decode_chain_in_replayed_graphs(gpu):
+    """The two block entry points with caller workspace (launch_mlp_block: RMSNorm
+    + two DMA GEMMs; launch_decode_mlp_int8: two split-K int8 streams + their
+    reductions) allocate and clear nothing, so they can be captured into a HIP
+    graph: every replay gives the eager bits, with eager launches and
+    synchronisations between the replays."""
+    import ctypes
+
+    import torch
+
+    from polykernel_amd import _lib, kernels, synth
+
+    lib = _lib.load()
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    M, d, F = 512, 1024, 4096
+    x = to_dev(synth.normal_bf16((M, d), 61))
+    g = to_dev(synth.normal_bf16((d,), 62, 0.1, 1.0))
+    w1 = to_dev(synth.normal_bf16((d, F), 63, 1 / np.sqrt(d)))
+    b1 = to_dev(synth.normal_bf16((F,), 64, 0.02))
+    w2 = to_dev(synth.normal_bf16((F, d), 65, 1 / np.sqrt(F)))
+    b2 = to_dev(synth.normal_bf16((d,), 66, 0.02))
+    ws = torch.empty(lib.pk_mlp_block_workspace_size(M, d, F), dtype=torch.uint8, device="cuda")
+
+    def mlp(out, sp):
+        return lib.launch_mlp_block(x.data_ptr(), g.data_ptr(), w1.data_ptr(), b1.data_ptr(), w2.data_ptr(),
+                                    b2.data_ptr(), out.data_ptr(), M, d, F, ctypes.c_float(1e-6),
+                                    ws.data_ptr(), ws.numel(), sp)
+
+    Md, dd, Fd = 16, 4096, 8192
+    xq = to_dev(synth.normal_bf16((Md, dd), 67))
+    w1q, s1 = kernels.quantize_per_channel(to_dev(synth.normal_bf16((dd, Fd), 68, 1 / np.sqrt(dd))))
+    w2q, s2 = kernels.quantize_per_channel(to_dev(synth.normal_bf16((Fd, dd), 69, 1 / np.sqrt(Fd))))
+    wsq = torch.empty(lib.pk_decode_mlp_int8_workspace_size(Md, dd, Fd), dtype=torch.uint8, device="cuda")
+
+    def decode(out, sp):
+        return lib.launch_decode_mlp_int8(xq.data_ptr(), w1q.data_ptr(), s1.data_ptr(), w2q.data_ptr(),
+                                          s2.data_ptr(), out.data_ptr(), Md, dd, Fd, wsq.data_ptr(),
+                                          wsq.numel(), sp)
+
+    for name, launch, shape in (("mlp_block", mlp, (M, d)), ("decode_mlp_int8", decode, (Md, dd))):
+        o = torch.empty(*shape, dtype=torch.bfloat16, device="cuda")
+        eager = torch.empty_like(o)
+        assert launch(eager, st()) == 0
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            assert launch(o, s.cuda_stream) == 0
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=s):
+                for _ in range(3):
+                    assert launch(o, torch.cuda.current_stream().cuda_stream) == 0
+        for rep in range(4):
+            o.fill_(0)
+            torch.cuda.synchronize()
+            gr.replay()
+            torch.cuda.synchronize()
+            _say(f"{name}: graph replay {rep}")
+            assert torch.equal(o.view(torch.int16), eager.view(torch.int16)), (name, rep)
+            assert launch(eager, st()) == 0  # eager work between replays
+            torch.cuda.synchronize()
